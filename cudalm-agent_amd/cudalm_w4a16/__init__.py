@@ -1,0 +1,228 @@
+"""Python host layer over the W4A16 engine's C ABI (include/cudalm_w4a16.h).
+
+Mirrors the reference's W4A16 operator interface for tests, the smoke check
+and benchmarks:
+
+  int4_gemv_bf16(weight, scales, x, y, N, K)              int4_gemv_bf16.h:46-48
+  batch_int4_gemv_bf16(weight, scale, x, y, N, K, B)      batch_decode.h:61-63
+  int4_gemv_bf16_rowtile4_regs()                          int4_gemv_bf16.h:52
+
+plus the load-time repack and the prepacked path. Arguments are torch
+tensors on the GPU (torch provides device memory and the stream; all
+arithmetic runs in the HIP library). Precondition violations raise
+ValueError (the reference aborts); launch failures raise RuntimeError.
+There is no fallback: if libcudalm_w4a16.so is missing, importing this
+module raises ImportError.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libcudalm_w4a16.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is not built; run `python cudalm-agent_amd/build.py` "
+        "(or __graft_entry__.build()) first")
+
+_lib = ctypes.CDLL(LIB_PATH)
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+
+_SIGS = {
+    "cudalm_w4a16_version": ([], _I),
+    "cudalm_w4a16_strerror": ([_I], ctypes.c_char_p),
+    "cudalm_w4a16_gemv_bf16": ([_P, _P, _P, _P, _I, _I, _I, _P], _I),
+    "cudalm_w4a16_gemv_bf16_variant": ([_P, _P, _P, _P, _I, _I, _I, _I, _P], _I),
+    "cudalm_w4a16_packed_bytes": ([_I, _I], _SZ),
+    "cudalm_w4a16_repack": ([_P, _P, _P, _I, _I, _P], _I),
+    "cudalm_w4a16_repack_host": ([_P, _P, _P, _I, _I], _I),
+    "cudalm_w4a16_gemv_bf16_prepacked": ([_P, _P, _P, _I, _I, _I, _P], _I),
+    "cudalm_w4a16_gemv_bf16_prepacked_variant": ([_P, _P, _P, _I, _I, _I, _I, _P], _I),
+    "cudalm_w4a16_dequant_f32": ([_P, _P, _P, _P, _I, _I, _P], _I),
+    "cudalm_w4a16_kernel_regs": ([_I], _I),
+}
+for _name, (_args, _ret) in _SIGS.items():
+    _fn = getattr(_lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = _ret
+
+EXPORTED_SYMBOLS = tuple(_SIGS)
+
+OK = 0
+EINVAL = -1
+ENULL = -2
+EALIGN = -3
+ELAUNCH = -4
+ERANGE = -5
+EVARIANT = -6
+
+VARIANT_AUTO = 0
+VARIANT_STREAM = 1
+VARIANT_TILE16 = 2
+VARIANT_TILE32 = 3
+VARIANT_PREFILL = 4
+VARIANT_BYTEWISE = 5
+VARIANTS = {
+    "auto": VARIANT_AUTO,
+    "stream": VARIANT_STREAM,
+    "tile16": VARIANT_TILE16,
+    "tile32": VARIANT_TILE32,
+    "prefill": VARIANT_PREFILL,
+    "bytewise": VARIANT_BYTEWISE,
+}
+
+GROUP = 128
+PACKED_BLOCK_BYTES = 1056
+
+
+class W4A16Error(RuntimeError):
+    def __init__(self, code: int, entry: str):
+        self.code = code
+        super().__init__(f"{entry}: {strerror(code)} (code {code})")
+
+
+def lib() -> ctypes.CDLL:
+    return _lib
+
+
+def version() -> int:
+    return _lib.cudalm_w4a16_version()
+
+
+def strerror(code: int) -> str:
+    return _lib.cudalm_w4a16_strerror(code).decode()
+
+
+def _check(rc: int, entry: str) -> None:
+    if rc == OK:
+        return
+    if rc in (EINVAL, ENULL, EALIGN, ERANGE, EVARIANT):
+        raise ValueError(f"{entry}: {strerror(rc)} (code {rc})")
+    raise W4A16Error(rc, entry)
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    import torch  # noqa: F401  (torch owns the streams)
+
+    if isinstance(stream, int):
+        return stream  # a raw hipStream_t (0 = the null stream)
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def packed_bytes(N: int, K: int) -> int:
+    return _lib.cudalm_w4a16_packed_bytes(N, K)
+
+
+def kernel_regs(variant: int = VARIANT_STREAM) -> int:
+    return _lib.cudalm_w4a16_kernel_regs(variant)
+
+
+# ---------------------------------------------------------------------------
+# raw-pointer layer (addresses are plain ints; used by the C-ABI tests)
+# ---------------------------------------------------------------------------
+
+def gemv_ptr(w: int, s: int, x: int, y: int, N: int, K: int, M: int,
+             variant: int = VARIANT_AUTO, stream: int | None = None) -> int:
+    return _lib.cudalm_w4a16_gemv_bf16_variant(w, s, x, y, N, K, M, variant, stream)
+
+
+def prepacked_ptr(p: int, x: int, y: int, N: int, K: int, M: int,
+                  variant: int = VARIANT_AUTO, stream: int | None = None) -> int:
+    return _lib.cudalm_w4a16_gemv_bf16_prepacked_variant(p, x, y, N, K, M, variant, stream)
+
+
+# ---------------------------------------------------------------------------
+# tensor layer
+# ---------------------------------------------------------------------------
+
+def _out(y, M: int, N: int, like):
+    import torch
+
+    if y is None:
+        y = torch.empty((M, N) if M > 1 else (N,), dtype=torch.bfloat16, device=like.device)
+    return y
+
+
+def gemv(weight, scale, x, N: int, K: int, M: int = 1, y=None, variant: int | str = VARIANT_AUTO,
+         stream=None):
+    """y[M, N] = W4A16(weight[N, K/2] u8, scale[N, K/128] fp16) @ x[M, K] bf16."""
+    if isinstance(variant, str):
+        variant = VARIANTS[variant]
+    y = _out(y, M, N, x)
+    rc = _lib.cudalm_w4a16_gemv_bf16_variant(_ptr(weight), _ptr(scale), _ptr(x), _ptr(y), N, K, M,
+                                             variant, _stream(stream))
+    _check(rc, "cudalm_w4a16_gemv_bf16")
+    return y
+
+
+def int4_gemv_bf16(weight, scales, x, y, N: int, K: int, stream=None):
+    """Reference name and argument order (int4_gemv_bf16.h:46-48)."""
+    return gemv(weight, scales, x, N, K, 1, y=y, stream=stream)
+
+
+def batch_int4_gemv_bf16(weight, scale, x, y, N: int, K: int, B: int, stream=None):
+    """Reference name and argument order (batch_decode.h:61-63)."""
+    return gemv(weight, scale, x, N, K, B, y=y, stream=stream)
+
+
+def int4_gemv_bf16_rowtile4_regs() -> int:
+    return kernel_regs(VARIANT_STREAM)
+
+
+def repack(weight, scale, N: int, K: int, out=None, stream=None):
+    """Device-side load-time repack; returns a uint8 tensor of packed_bytes(N, K)."""
+    import torch
+
+    if out is None:
+        out = torch.empty(packed_bytes(N, K), dtype=torch.uint8, device=weight.device)
+    rc = _lib.cudalm_w4a16_repack(_ptr(weight), _ptr(scale), _ptr(out), N, K, _stream(stream))
+    _check(rc, "cudalm_w4a16_repack")
+    return out
+
+
+def repack_host(weight_np, scale_bits_np, N: int, K: int):
+    """Host-side repack of numpy arrays (uint8 [N, K/2], uint16 [N, K/128])."""
+    import numpy as np
+
+    w = np.ascontiguousarray(weight_np, dtype=np.uint8)
+    s = np.ascontiguousarray(scale_bits_np, dtype=np.uint16)
+    out = np.empty(packed_bytes(N, K), dtype=np.uint8)
+    rc = _lib.cudalm_w4a16_repack_host(w.ctypes.data, s.ctypes.data, out.ctypes.data, N, K)
+    _check(rc, "cudalm_w4a16_repack_host")
+    return out
+
+
+def gemv_prepacked(packed, x, N: int, K: int, M: int = 1, y=None,
+                   variant: int | str = VARIANT_AUTO, stream=None):
+    if isinstance(variant, str):
+        variant = VARIANTS[variant]
+    y = _out(y, M, N, x)
+    rc = _lib.cudalm_w4a16_gemv_bf16_prepacked_variant(_ptr(packed), _ptr(x), _ptr(y), N, K, M,
+                                                       variant, _stream(stream))
+    _check(rc, "cudalm_w4a16_gemv_bf16_prepacked")
+    return y
+
+
+def dequant(weight, scale, N: int, K: int, want_q: bool = True, want_w: bool = True, stream=None):
+    """(q int8 [N, K], w fp32 [N, K]) through the kernels' nibble decoder."""
+    import torch
+
+    q = torch.empty((N, K), dtype=torch.int8, device=weight.device) if want_q else None
+    w = torch.empty((N, K), dtype=torch.float32, device=weight.device) if want_w else None
+    rc = _lib.cudalm_w4a16_dequant_f32(_ptr(weight), _ptr(scale), _ptr(q), _ptr(w), N, K,
+                                       _stream(stream))
+    _check(rc, "cudalm_w4a16_dequant_f32")
+    return q, w

@@ -1,0 +1,130 @@
+/*
+ * cudalm_w4a16 -- C ABI of the MI355X (gfx950) W4A16 projection engine.
+ *
+ * Arithmetic contract (the reference's, include/cudalm/kernels/
+ * int4_gemv_bf16.h:6-9,29-37):
+ *
+ *   y[m, n] = bf16_rne( sum_k q[n, k] * f32(scale_fp16[n, k / 128]) * f32(x[m, k]) )
+ *
+ *   weight : packed int4 [N, K/2] uint8, row-major. Low nibble of byte b is
+ *            element k = 2b, high nibble is k = 2b+1, 4-bit two's complement.
+ *   scale  : fp16 bit patterns [N, K/128], row-major (the stored fp16 scale
+ *            is the contract, docs/weight_format.md:135-153).
+ *   x      : bf16 bit patterns [M, K], row-major (M activation rows).
+ *   y      : bf16 bit patterns [M, N], row-major.
+ *
+ * Accumulation is fp32; the output is rounded once to bf16 (round to
+ * nearest even). Results are within 2 bf16 ulp of an fp32-accumulated
+ * reference plus a floor for outputs that cancel (the tests state it).
+ * Every entry point computes row m of a batched call bit-identically to a
+ * single-row call on row m, whichever kernel (M = 1 stream, small-M tile,
+ * prefill tile) and weight layout (file or prepacked) serves it.
+ *
+ * Ownership and threading: the caller owns every buffer. Entry points keep
+ * no state, never synchronize, and enqueue asynchronously on `stream`.
+ * Device pointers must be device-accessible; misaligned weight / x bases
+ * are accepted (a byte-wise fallback kernel serves them), as the reference
+ * requires (int4_gemv_bf16.h:39-45).
+ *
+ * Error model: each call returns 0 or a negative CUDALM_W4A16_E* code and
+ * leaves the stream untouched on a precondition failure. The C++ wrappers
+ * under include/cudalm/ turn a nonzero code into the reference's fatal
+ * abort (cuda_check.h:53-63).
+ */
+#ifndef CUDALM_W4A16_H
+#define CUDALM_W4A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CUDALM_W4A16_OK 0
+#define CUDALM_W4A16_EINVAL (-1)  /* N < 1, M < 1, K <= 0 or K % 128 != 0 */
+#define CUDALM_W4A16_ENULL (-2)   /* a required pointer is NULL */
+#define CUDALM_W4A16_EALIGN (-3)  /* a prepacked buffer is not 16 B aligned */
+#define CUDALM_W4A16_ELAUNCH (-4) /* the HIP runtime rejected a launch */
+#define CUDALM_W4A16_ERANGE (-5)  /* sizes overflow the kernels' index range */
+#define CUDALM_W4A16_EVARIANT (-6) /* unknown kernel variant id */
+
+#define CUDALM_W4A16_GROUP 128
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int cudalm_w4a16_version(void);
+
+/* Human-readable text for a return code. Never NULL. */
+const char* cudalm_w4a16_strerror(int code);
+
+/* y[M, N] = W4A16(weight, scale) applied to x[M, K], file weight layout.
+ * Replaces int4_gemv_bf16 (M == 1; include/cudalm/kernels/
+ * int4_gemv_bf16.h:46-48) and kernels::batch_int4_gemv_bf16 (M == B;
+ * include/cudalm/kernels/batch_decode.h:61-63), and serves prefill chunks
+ * (M >= 64), which the reference runs one token at a time. */
+int cudalm_w4a16_gemv_bf16(const uint8_t* weight, const uint16_t* scale,
+                           const uint16_t* x, uint16_t* y, int N, int K, int M,
+                           hipStream_t stream);
+
+/* Bytes of the prepacked (load-time repacked) form of an [N, K] weight:
+ * ceil(N/16) * (K/128) * 1056. 0 on invalid shape. */
+size_t cudalm_w4a16_packed_bytes(int N, int K);
+
+/* Load-time repack, device to device (stream-ordered). `packed` must hold
+ * cudalm_w4a16_packed_bytes(N, K) bytes, 16 B aligned. The hook the
+ * reference's loader would call next to its upload lambda
+ * (src/runtime/weight_loader_v2.cpp:435-441). */
+int cudalm_w4a16_repack(const uint8_t* weight, const uint16_t* scale,
+                        void* packed, int N, int K, hipStream_t stream);
+
+/* The same repack on host memory (for loaders that hold the file bytes on
+ * the host before the upload). Byte-identical to cudalm_w4a16_repack. */
+int cudalm_w4a16_repack_host(const uint8_t* weight, const uint16_t* scale,
+                             void* packed, int N, int K);
+
+/* y[M, N] from a prepacked weight. Bit-identical to cudalm_w4a16_gemv_bf16
+ * on the file layout it was packed from. `packed` and `x` must be 16 B
+ * aligned (x may not be: then EALIGN). */
+int cudalm_w4a16_gemv_bf16_prepacked(const void* packed, const uint16_t* x,
+                                     uint16_t* y, int N, int K, int M,
+                                     hipStream_t stream);
+
+/* Dequantize through the kernels' own nibble decoder: q_out[N, K] int8 and
+ * w_out[N, K] = q * f32(scale) (either output may be NULL). The weight base
+ * must be 4 B aligned. Equivalent to the reference's dequant_reference
+ * (tools/common/w4a16_quant.py:74-82). */
+int cudalm_w4a16_dequant_f32(const uint8_t* weight, const uint16_t* scale,
+                             int8_t* q_out, float* w_out, int N, int K,
+                             hipStream_t stream);
+
+/* Kernel variants, for parity tests and benchmarks (the counterpart of the
+ * reference's explicit per-variant launchers, include/cudalm/kernels/
+ * int4_gemv_qwen35.h:59-83). Every variant is bit-identical per output to
+ * the default dispatch except CUDALM_W4A16_VARIANT_BYTEWISE, which sums in
+ * the reference's order and is within tolerance. */
+#define CUDALM_W4A16_VARIANT_AUTO 0
+#define CUDALM_W4A16_VARIANT_STREAM 1   /* M <= 16, x resident in LDS */
+#define CUDALM_W4A16_VARIANT_TILE16 2   /* 16 columns per wave, K chunked */
+#define CUDALM_W4A16_VARIANT_TILE32 3   /* 32 columns per wave, K chunked */
+#define CUDALM_W4A16_VARIANT_PREFILL 4  /* 64x64 per wave, 128x128 per group */
+#define CUDALM_W4A16_VARIANT_BYTEWISE 5 /* misaligned-base fallback */
+int cudalm_w4a16_gemv_bf16_variant(const uint8_t* weight, const uint16_t* scale,
+                                   const uint16_t* x, uint16_t* y, int N, int K,
+                                   int M, int variant, hipStream_t stream);
+int cudalm_w4a16_gemv_bf16_prepacked_variant(const void* packed,
+                                             const uint16_t* x, uint16_t* y,
+                                             int N, int K, int M, int variant,
+                                             hipStream_t stream);
+
+/* VGPR + AGPR count of a variant's kernel, -1 if unavailable. Replaces
+ * int4_gemv_bf16_rowtile4_regs (int4_gemv_bf16.h:52) and
+ * batch_int4_gemv_bf16_rowtile4_regs (batch_decode.h:67). */
+int cudalm_w4a16_kernel_regs(int variant);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

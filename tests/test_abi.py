@@ -1,0 +1,139 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/cudalm_w4a16.h declares, rejects bad shapes before touching the
+device, computes the packed size and host repack layout, and the C++
+entry points with the reference's names abort on a violated precondition
+(the reference's CUDALM_PRECONDITION model, cuda_check.h:53-63)."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "cudalm_w4a16.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(cudalm_w4a16_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(w4):
+    syms = declared_symbols()
+    assert len(syms) >= 10
+    for s in syms:
+        assert hasattr(w4.lib(), s), s
+    assert set(syms) == set(w4.EXPORTED_SYMBOLS)
+
+
+def test_version_and_strerror(w4):
+    assert w4.version() >= 100
+    for code in range(-6, 1):
+        assert w4.strerror(code)
+    assert "unknown" in w4.strerror(-99)
+
+
+def test_shape_preconditions_rejected_before_device(w4):
+    # invalid shapes and null pointers return before any HIP call
+    fake = 0x1000
+    assert w4.gemv_ptr(fake, fake, fake, fake, 0, 128, 1) == w4.EINVAL
+    assert w4.gemv_ptr(fake, fake, fake, fake, 4, 100, 1) == w4.EINVAL
+    assert w4.gemv_ptr(fake, fake, fake, fake, 4, 0, 1) == w4.EINVAL
+    assert w4.gemv_ptr(fake, fake, fake, fake, 4, 128, 0) == w4.EINVAL
+    assert w4.gemv_ptr(None, fake, fake, fake, 4, 128, 1) == w4.ENULL
+    assert w4.prepacked_ptr(fake, fake, fake, 4, 127, 1) == w4.EINVAL
+    assert w4.prepacked_ptr(fake + 8, fake, fake, 4, 128, 1) == w4.EALIGN
+    lib = w4.lib()
+    assert lib.cudalm_w4a16_repack(fake, fake, fake, 0, 128, None) == w4.EINVAL
+    assert lib.cudalm_w4a16_repack(fake, fake, fake + 4, 16, 128, None) == w4.EALIGN
+    assert lib.cudalm_w4a16_dequant_f32(fake + 1, fake, None, None, 16, 128, None) == w4.EALIGN
+    # misaligned bases are legal for the file-layout entry, but not with a
+    # vectorized variant forced
+    assert w4.gemv_ptr(fake + 1, fake, fake, fake, 4, 128, 1, w4.VARIANT_STREAM) == w4.EVARIANT
+
+
+def test_packed_bytes(w4):
+    assert w4.packed_bytes(16, 128) == 1056
+    assert w4.packed_bytes(17, 128) == 2 * 1056
+    assert w4.packed_bytes(248320, 1024) == 15520 * 8 * 1056
+    assert w4.packed_bytes(0, 128) == 0
+    assert w4.packed_bytes(16, 100) == 0
+
+
+def _numpy_repack(W, S, N, K):
+    G = K // 128
+    nt = (N + 15) // 16
+    Wp = np.zeros((nt * 16, K // 2), np.uint8)
+    Wp[:N] = W
+    Sp = np.zeros((nt * 16, G), np.uint16)
+    Sp[:N] = S
+    out = np.zeros((nt, G, 1056), np.uint8)
+    for rt in range(nt):
+        for g in range(G):
+            for lane in range(64):
+                i, a = lane & 15, lane >> 4
+                out[rt, g, 16 * lane:16 * lane + 16] = Wp[rt * 16 + i, g * 64 + a * 16:g * 64 + a * 16 + 16]
+            out[rt, g, 1024:] = np.ascontiguousarray(Sp[rt * 16:rt * 16 + 16, g]).view(np.uint8)
+    return out.ravel()
+
+
+@pytest.mark.parametrize("N,K", [(1, 128), (16, 256), (37, 384), (64, 1024)])
+def test_repack_host_layout(w4, orc, N, K):
+    W, S, _ = orc.fixture_gemv(N + K, N, K)
+    got = w4.repack_host(W, S, N, K)
+    assert np.array_equal(got, _numpy_repack(W, S, N, K))
+
+
+def test_cpp_headers_compile_and_link(tmp_path, w4):
+    src = tmp_path / "use.cpp"
+    src.write_text(r'''
+#include "cudalm/kernels/int4_gemv_bf16.h"
+#include "cudalm/kernels/batch_decode.h"
+#include "cudalm/w4a16_linear.h"
+#include "cudalm_w4a16.h"
+#include <cstdio>
+int main() {
+  std::printf("%zu %zu\n", cudalm::packed_w4a16_bytes(16, 128), cudalm_w4a16_packed_bytes(32, 256));
+  return 0;
+}
+''')
+    exe = tmp_path / "use"
+    libdir = os.path.dirname(w4.LIB_PATH)
+    cmd = ["/opt/rocm/bin/hipcc", "-std=c++17", "-I", os.path.join(REPO, "include"), str(src),
+           "-L", libdir, "-lcudalm_w4a16", f"-Wl,-rpath,{libdir}", "-o", str(exe)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.split() == ["1056", str(2 * 2 * 1056)]
+
+
+def test_cpp_entry_aborts_on_precondition(tmp_path, w4):
+    src = tmp_path / "bad.cpp"
+    src.write_text(r'''
+#include "cudalm/kernels/int4_gemv_bf16.h"
+int main() {
+  // K % 128 != 0: the reference aborts (int4_gemv_bf16.cu:224-226)
+  cudalm::int4_gemv_bf16(nullptr, nullptr, nullptr, nullptr, 8, 100, nullptr);
+  return 0;
+}
+''')
+    exe = tmp_path / "bad"
+    libdir = os.path.dirname(w4.LIB_PATH)
+    cmd = ["/opt/rocm/bin/hipcc", "-std=c++17", "-I", os.path.join(REPO, "include"), str(src),
+           "-L", libdir, "-lcudalm_w4a16", f"-Wl,-rpath,{libdir}", "-o", str(exe)]
+    assert subprocess.run(cmd, capture_output=True).returncode == 0
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert res.returncode != 0
+    assert "invalid shape" in res.stderr
+
+
+def test_python_layer_raises_on_bad_shape(w4):
+    import torch
+
+    x = torch.zeros(128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        w4.gemv(x, x, x, 0, 128, 1, y=x, stream=0)

@@ -1,0 +1,243 @@
+"""GPU parity tests: the HIP kernels, called through the C ABI, against the
+CPU oracle (a restatement of the reference's ref_gemv_bf16,
+tests/cuda/test_int4_gemv_bf16.cpp:54-69) on the reference's own fixture
+recipes, shapes, seeds and input classes
+(tests/cuda/test_w4a16_qwen35_optimized.cpp:66-171,456).
+
+Bars:
+  * unpack and dequantized weights: bit-exact;
+  * outputs: |y - r| <= 2 ulp_bf16(r) + 2^-16 * sum_k |q s x|, with r the
+    fp64 sum of the exact fp32 terms (oracle.check_tolerance); the count of
+    elements beyond 2 ulp is reported and must be 0 outside cancellation;
+  * every kernel variant, both weight layouts and every batch row:
+    bit-identical per output (the reference's row-parity and variant
+    bit-identity gates, test_w4a16_qwen35_optimized.cpp:1-35).
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+# census (benchmarks/profiling/v07b_w4a16_shape_census.txt) + edge shapes
+# (test_w4a16_qwen35_optimized.cpp:154-171)
+CENSUS = [(16, 1024), (512, 1024), (1024, 2048), (1024, 3584), (2048, 1024), (3584, 1024),
+          (4096, 1024), (6144, 1024)]
+EDGE = [(1, 128), (3, 128), (5, 256), (9, 1024), (15, 1024), (1023, 1024)]
+VARIANTS_FOR_M = {
+    # variant name -> predicate on (M, K) for applicability
+    "stream": lambda M, K: M <= 16 and M * (K // 8 + 1) * 16 + ((M * (K // 128) + 3) & ~3) * 4 + 4096 <= 65536,
+    "tile16": lambda M, K: True,
+    "tile32": lambda M, K: True,
+    "prefill": lambda M, K: True,
+}
+
+
+def up(dev, W, S, X):
+    w = torch.from_numpy(np.ascontiguousarray(W)).to(dev)
+    s = torch.from_numpy(np.ascontiguousarray(S).view(np.int16)).to(dev).view(torch.float16)
+    x = torch.from_numpy(np.ascontiguousarray(X).view(np.int16)).to(dev).view(torch.bfloat16)
+    return w, s, x
+
+
+def down(t):
+    torch.cuda.synchronize()
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def run(w4, w, s, x, N, K, M, variant="auto"):
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=w.device)
+    w4.gemv(w, s, x, N, K, M, y=y, variant=variant)
+    return down(y).reshape(M, N)
+
+
+def assert_tol(orc, Y, W, S, X, N, K, M, label=""):
+    ok, st = orc.check_tolerance(Y, W, S, X, N, K, M)
+    print(f"  {label} N={N} K={K} M={M}: {st}", flush=True)
+    assert ok, (label, st)
+    return st
+
+
+# ---------------------------------------------------------------- dequant ---
+
+@pytest.mark.parametrize("N,K,kind", [(16, 1024, "random"), (3, 128, "boundary"),
+                                      (37, 256, "random"), (512, 1024, "boundary"),
+                                      (1023, 1024, "small")])
+def test_dequant_bitexact(w4, orc, dev, N, K, kind):
+    W, S, _ = orc.fixture_kind(kind, 0x51ED, N, K, 1)
+    w, s, _ = up(dev, W, S, np.zeros((1, K), np.uint16))
+    q, wf = w4.dequant(w, s, N, K)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), orc.unpack(W, N, K))
+    assert np.array_equal(wf.cpu().numpy().view(np.uint32), orc.dequant(W, S, N, K).view(np.uint32))
+
+
+# ---------------------------------------------------------------- reference's GEMV tests ---
+
+@pytest.mark.parametrize("N,K", [(4096, 1024), (512, 1024), (1024, 2048), (3584, 1024),
+                                 (1024, 3584), (16, 1024), (3, 128)])
+def test_reference_vectorized_shapes(w4, orc, dev, N, K):
+    # test_int4_gemv_bf16.cpp:127-140, seed 0x51ed51 + N + K
+    W, S, X = orc.fixture_gemv(0x51ED51 + N + K, N, K)
+    Y = run(w4, *up(dev, W, S, X), N, K, 1)
+    assert_tol(orc, Y, W, S, X, N, K, 1, "vectorized")
+    if orc.ref is not None:
+        ok, mx, idx = orc.ref.compare_bf16_stages(orc.gemv_bf16(W, S, X, N, K), Y)
+        assert ok, (mx, idx)
+
+
+def test_zero_group_exact_zero(w4, orc, dev):
+    # test_int4_gemv_bf16.cpp:146-176
+    N, K = 8, 256
+    W = np.zeros((N, K // 2), np.uint8)
+    S = np.zeros((N, K // 128), np.uint16)
+    X = orc.f32_to_bf16((orc.xorshift32(123, K) * (2.0 / 4294967296.0) - 1.0).astype(np.float32))
+    X = X.reshape(1, K)
+    for M in (1, 3, 40):
+        Xm = np.repeat(X, M, axis=0)
+        Y = run(w4, *up(dev, W, S, Xm), N, K, M)
+        assert not Y.any()
+    # zero scales with nonzero nibbles also give exact zeros
+    W2 = np.full((N, K // 2), 0x77, np.uint8)
+    Y = run(w4, *up(dev, W2, S, X), N, K, 1)
+    assert not Y.any()
+
+
+def test_misaligned_bases_take_bytewise_path(w4, orc, dev):
+    # test_int4_gemv_bf16.cpp:181-242: W and x offset by one byte
+    N, K = 37, 256
+    W, S, X = orc.fixture_gemv(777, N, K)
+    wbuf = torch.zeros(W.size + 2, dtype=torch.uint8, device=dev)
+    wbuf[1:1 + W.size] = torch.from_numpy(W.ravel()).to(dev)
+    xbytes = X.view(np.uint8).ravel()
+    xbuf = torch.zeros(xbytes.size + 2, dtype=torch.uint8, device=dev)
+    xbuf[1:1 + xbytes.size] = torch.from_numpy(xbytes).to(dev)
+    s = torch.from_numpy(S.view(np.int16)).to(dev)
+    y = torch.empty(N, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = w4.gemv_ptr(wbuf.data_ptr() + 1, s.data_ptr(), xbuf.data_ptr() + 1, y.data_ptr(), N, K, 1,
+                     w4.VARIANT_AUTO, stream)
+    assert rc == 0
+    Yb = down(y).reshape(1, N)
+    assert_tol(orc, Yb, W, S, X, N, K, 1, "bytewise")
+    Yv = run(w4, *up(dev, W, S, X), N, K, 1)
+    if orc.ref is not None:
+        ok, mx, _ = orc.ref.compare_bf16_stages(Yv, Yb)
+        assert ok, mx
+
+
+# ---------------------------------------------------------------- variant / row parity gate ---
+
+def _parity_case(w4, orc, dev, N, K, B, kind, seed):
+    W, S, X = orc.fixture_kind(kind, seed, N, K, B)
+    w, s, x = up(dev, W, S, X)
+    Y = run(w4, w, s, x, N, K, B)
+    assert_tol(orc, Y, W, S, X, N, K, B, f"{kind}/{seed:#x}")
+    # row parity: batch row b == single call on row b
+    for b in range(B):
+        yb = run(w4, w, s, x[b:b + 1], N, K, 1)
+        assert np.array_equal(Y[b], yb[0]), ("row parity", b)
+    # every applicable variant, file layout and prepacked
+    p = w4.repack(w, s, N, K)
+    for name, ok in VARIANTS_FOR_M.items():
+        if not ok(B, K):
+            continue
+        assert np.array_equal(run(w4, w, s, x, N, K, B, name), Y), ("variant", name)
+        yp = torch.empty((B, N), dtype=torch.bfloat16, device=dev)
+        w4.gemv_prepacked(p, x, N, K, B, y=yp, variant=name)
+        assert np.array_equal(down(yp).reshape(B, N), Y), ("prepacked", name)
+
+
+@pytest.mark.parametrize("N,K", EDGE + CENSUS[:2])
+@pytest.mark.parametrize("kind", ["random", "zero", "small", "mixed_sign", "boundary"])
+def test_parity_gate_small(w4, orc, dev, N, K, kind):
+    for seed in orc.REFERENCE_SEEDS:
+        _parity_case(w4, orc, dev, N, K, 3, kind, seed)
+
+
+@pytest.mark.parametrize("N,K", CENSUS[2:])
+@pytest.mark.parametrize("kind", ["random", "boundary", "mixed_sign"])
+def test_parity_gate_census(w4, orc, dev, N, K, kind):
+    _parity_case(w4, orc, dev, N, K, 3, kind, 0x1234ABCD)
+
+
+# ---------------------------------------------------------------- BASELINE workloads ---
+
+@pytest.mark.parametrize("N,K", CENSUS)
+@pytest.mark.parametrize("M", [1, 8, 32])
+def test_census_synthetic(w4, orc, dev, N, K, M):
+    # N(0, 0.02) weights quantized per 128-group,
+    # N(0, 1) bf16 activations, per-shape seeds
+    W, S = orc.synth_w4a16(0xC0DA0000 + N + K, N, K)
+    X = orc.synth_act(0xAC7 + M, M, K)
+    Y = run(w4, *up(dev, W, S, X), N, K, M)
+    st = assert_tol(orc, Y, W, S, X, N, K, M, "census")
+    assert st["n_over_2ulp"] <= max(1, st["n"] // 10000)
+
+
+@pytest.mark.parametrize("N,K", [(3584, 1024), (1024, 3584), (16, 1024), (6144, 1024)])
+@pytest.mark.parametrize("M", [64, 100, 512])
+def test_prefill_chunks(w4, orc, dev, N, K, M):
+    # M-token prefill chunk GEMM
+    W, S = orc.synth_w4a16(0xBEEF + N + K, N, K)
+    X = orc.synth_act(0xF00D + M, M, K)
+    w, s, x = up(dev, W, S, X)
+    Y = run(w4, w, s, x, N, K, M)
+    assert_tol(orc, Y, W, S, X, N, K, M, "prefill")
+    for b in (0, 17, M - 1):
+        assert np.array_equal(Y[b], run(w4, w, s, x[b:b + 1], N, K, 1)[0]), b
+
+
+def test_lm_head_full_size(w4, orc, dev):
+    # N = 248320, K = 1024, M = 1, whole output checked
+    N, K = 248320, 1024
+    W, S = orc.synth_w4a16(0x11AD, N, K)
+    X = orc.synth_act(0x11AE, 1, K)
+    w, s, x = up(dev, W, S, X)
+    Y = run(w4, w, s, x, N, K, 1)
+    st = assert_tol(orc, Y, W, S, X, N, K, 1, "lm_head")
+    assert st["n_over_2ulp"] <= N // 10000
+    p = w4.repack(w, s, N, K)
+    yp = w4.gemv_prepacked(p, x, N, K, 1)
+    assert np.array_equal(down(yp).reshape(1, N), Y)
+    # checksum of a second activation row: linearity in x (y(2x) == 2 y(x))
+    x2 = (x.float() * 2).to(torch.bfloat16)
+    Y2 = run(w4, w, s, x2, N, K, 1)
+    assert np.array_equal(orc.bf16_to_f32(Y2), orc.bf16_to_f32(Y) * 2)
+
+
+def test_repack_device_equals_host(w4, orc, dev):
+    for N, K in ((1, 128), (37, 384), (1023, 1024), (16, 3584)):
+        W, S, _ = orc.fixture_gemv(N * 7 + K, N, K)
+        w, s, _ = up(dev, W, S, np.zeros((1, K), np.uint16))
+        p = w4.repack(w, s, N, K)
+        torch.cuda.synchronize()
+        assert np.array_equal(p.cpu().numpy(), w4.repack_host(W, S, N, K)), (N, K)
+
+
+def test_nondefault_stream(w4, orc, dev):
+    N, K, M = 3584, 1024, 8
+    W, S, X = orc.fixture_gemv(99, N, K)
+    X = np.repeat(X, M, axis=0)
+    w, s, x = up(dev, W, S, X)
+    ref = run(w4, w, s, x, N, K, M)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        w4.gemv(w, s, x, N, K, M, y=y, stream=st)
+    st.synchronize()
+    assert np.array_equal(down(y).reshape(M, N), ref)
+
+
+def test_cpp_reference_names(w4, orc, dev):
+    # int4_gemv_bf16 / batch_int4_gemv_bf16 in the reference's argument order
+    N, K, B = 512, 1024, 3
+    W, S, X = orc.fixture_kind("random", 0x9E3779B9, N, K, B)
+    w, s, x = up(dev, W, S, X)
+    y1 = torch.empty(N, dtype=torch.bfloat16, device=dev)
+    w4.int4_gemv_bf16(w, s, x[0], y1, N, K)
+    yb = torch.empty((B, N), dtype=torch.bfloat16, device=dev)
+    w4.batch_int4_gemv_bf16(w, s, x, yb, N, K, B)
+    assert np.array_equal(down(yb).reshape(B, N)[0], down(y1).reshape(N))
+    assert w4.int4_gemv_bf16_rowtile4_regs() > 0
