@@ -1,0 +1,328 @@
+"""W4A16 projection benchmark on one MI355X.
+
+Headline: the LM-head GEMV, M = 1, K = 1024,
+N = 248320, W4A16 G=128 (N(0, 0.02) weights quantized per group, fp16
+scales, bf16 activation ~ N(0, 1)), through the production path: the
+load-time repacked weights (cudalm_w4a16_gemv_bf16_prepacked). One step =
+one GEMV launch. Four weight copies rotate so each step streams from HBM
+and not from the 256 MB MALL. `value` = algorithmic bytes per step /
+measured time per step (GB/s).
+
+Also reported (same JSON line, extra keys):
+  * the file-layout entry (cudalm_w4a16_gemv_bf16) on the same workload;
+  * configs[0] (M=1, 3584x1024) per-launch time;
+  * configs[2-3]: the 24-layer decode projection census (186 calls + LM
+    head) at M = 1, 8, 32, replayed from a HIP graph: us per decode step,
+    and aggregate GB/s;
+  * prefill-chunk GEMM, M = 512, per census shape: TFLOP/s;
+  * cpu_baseline: the oracle's restatement of the reference's CPU path
+    (ref_gemv_bf16) on the host cores, LM-head workload.
+
+Synthetic data is generated with torch on the GPU (seeded), not read
+from disk. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "cudalm-agent_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "W4A16 GEMV achieved HBM GB/s (% peak) at M=1/8; µs per decode-step projections"
+
+# 24-layer Qwen3.5-0.8B projection census, per layer in call order
+# (benchmarks/profiling/v07b_w4a16_shape_census.txt; src/runtime/
+# qwen35_deltanet.cpp:166-251, qwen35_full_attention.cpp:211-340).
+DELTANET = [("in_proj_qkv", 6144, 1024), ("in_proj_z", 2048, 1024), ("in_proj_b", 16, 1024),
+            ("in_proj_a", 16, 1024), ("out_proj", 1024, 2048)]
+FULL_ATTN = [("q_proj", 4096, 1024), ("k_proj", 512, 1024), ("v_proj", 512, 1024),
+             ("o_proj", 1024, 2048)]
+MLP = [("gate_proj", 3584, 1024), ("up_proj", 3584, 1024), ("down_proj", 1024, 3584)]
+LM_HEAD = (248320, 1024)
+
+
+def layer_kinds():
+    # full attention at every 4th layer (3, 7, ..., 23): 6 full, 18 DeltaNet
+    return ["full" if (i % 4) == 3 else "delta" for i in range(24)]
+
+
+def census_calls():
+    calls = []
+    for li, kind in enumerate(layer_kinds()):
+        for name, N, K in (FULL_ATTN if kind == "full" else DELTANET) + MLP:
+            calls.append((li, name, N, K))
+    return calls
+
+
+def algo_bytes(N: int, K: int, M: int) -> int:
+    return N * K // 2 + 2 * N * K // 128 + 2 * M * K + 2 * M * N
+
+
+def synth_weights(torch, N: int, K: int, seed: int, dev):
+    """N(0, 0.02) fp32 -> reference quantizer (docs/weight_format.md:135-153)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    Wf = torch.randn((N, K), generator=g, device=dev, dtype=torch.float32) * 0.02
+    Wg = Wf.view(N, K // 128, 128)
+    s32 = Wg.abs().amax(dim=2) / 7
+    zero = s32 == 0
+    safe = torch.where(zero, torch.ones_like(s32), s32)
+    q = torch.round(Wg / safe.unsqueeze(2)).clamp_(-7, 7)
+    q = torch.where(zero.unsqueeze(2), torch.zeros_like(q), q).view(N, K).to(torch.int32)
+    packed = (((q[:, 1::2] & 15) << 4) | (q[:, 0::2] & 15)).to(torch.uint8).contiguous()
+    scale = s32.to(torch.float16).contiguous()
+    del Wf, Wg, q
+    return packed, scale
+
+
+def synth_act(torch, M: int, K: int, seed: int, dev):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16).contiguous()
+
+
+def time_launches(torch, launches, reps: int, warmup: int, stream):
+    """Run `launches` (callables) round-robin; returns (avg seconds per launch
+    from per-launch event pairs, total seconds for `reps` launches)."""
+    for i in range(warmup):
+        launches[i % len(launches)]()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(reps):
+        starts[i].record(stream)
+        launches[i % len(launches)]()
+        ends[i].record(stream)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    per = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / reps * 1e-3
+    return per, t0.elapsed_time(t1) * 1e-3
+
+
+def graph_time(torch, fn, reps: int, stream):
+    """Capture fn() into a HIP graph, replay `reps` times; seconds per replay."""
+    g = torch.cuda.CUDAGraph()
+    fn()  # warm
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(reps):
+        g.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e-3 / reps
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=4, help="rotating weight copies (> MALL)")
+    ap.add_argument("--no-census", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the W4A16 projection path runs on a single "
+              "MI355X here (multi-GPU sharding along N is described in DESIGN.md, not run).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import cudalm_w4a16 as w4
+
+    dev = torch.device("cuda:0")
+    # one non-default stream carries every launch (graph capture needs one)
+    stream = torch.cuda.Stream(device=dev)
+    torch.cuda.set_stream(stream)
+    sraw = stream.cuda_stream
+    lib = w4.lib()
+
+    # ---------------- headline: LM head, M = 1, prepacked ----------------
+    N, K = LM_HEAD
+    M = 1
+    packs, ws, ss = [], [], []
+    for c in range(args.copies):
+        w, s = synth_weights(torch, N, K, 0x11AD + c, dev)
+        packs.append(w4.repack(w, s, N, K))
+        ws.append(w)
+        ss.append(s)
+    x = synth_act(torch, M, K, 0x11AE, dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    xp, yp = x.data_ptr(), y.data_ptr()
+
+    def mk_packed(p):
+        pp = p.data_ptr()
+        return lambda: lib.cudalm_w4a16_gemv_bf16_prepacked(pp, xp, yp, N, K, M, sraw)
+
+    def mk_file(w, s):
+        wp_, sp_ = w.data_ptr(), s.data_ptr()
+        return lambda: lib.cudalm_w4a16_gemv_bf16(wp_, sp_, xp, yp, N, K, M, sraw)
+
+    # the timed region: K steps bracketed by synchronize on both sides
+    launches = [mk_packed(p) for p in packs]
+    per_launch, _ = time_launches(torch, launches, min(args.steps, 100), args.warmup, stream)
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for i in range(args.steps):
+        launches[i % len(launches)]()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    step_s = elapsed / args.steps
+    nbytes = algo_bytes(N, K, M)
+    value = nbytes / step_s / 1e9
+    kern_gbs = nbytes / per_launch / 1e9
+
+    file_per, _ = time_launches(torch, [mk_file(w, s) for w, s in zip(ws, ss)],
+                                min(args.steps, 100), args.warmup, stream)
+    file_gbs = nbytes / file_per / 1e9
+
+    # M = 1, N = 3584, K = 1024 (rotate 64 copies = 120 MB; a
+    # single 1.9 MB matrix would be served from cache)
+    N0, K0 = 3584, 1024
+    c0 = []
+    for c in range(64):
+        w, s = synth_weights(torch, N0, K0, 0x3584 + c, dev)
+        c0.append(w4.repack(w, s, N0, K0))
+    x0 = synth_act(torch, 1, K0, 0x3585, dev)
+    y0 = torch.empty((1, N0), dtype=torch.bfloat16, device=dev)
+    x0p, y0p = x0.data_ptr(), y0.data_ptr()
+    c0_launch = [(lambda pp=p.data_ptr(): lib.cudalm_w4a16_gemv_bf16_prepacked(pp, x0p, y0p, N0, K0, 1, sraw))
+                 for p in c0]
+    cfg0_s = graph_time(torch, lambda: [f() for f in c0_launch], 20, stream) / len(c0_launch)
+    del c0
+
+    extra = {}
+    # ---------------- census: 186 calls + LM head per decode step ----------------
+    if not args.no_census:
+        calls = census_calls()
+        cw = {}
+        for li, name, Nc, Kc in calls:
+            w, s = synth_weights(torch, Nc, Kc, 0xC0DA0000 + 16 * li + len(name), dev)
+            cw[(li, name)] = w4.repack(w, s, Nc, Kc)
+        census = {}
+        for Mc in (1, 8, 32):
+            xs = {Kc: synth_act(torch, Mc, Kc, 0xAC70 + Kc + Mc, dev) for Kc in (1024, 2048, 3584)}
+            ys = {}
+            for _, name, Nc, Kc in calls:
+                ys.setdefault(Nc, torch.empty((Mc, Nc), dtype=torch.bfloat16, device=dev))
+            xh = synth_act(torch, Mc, K, 0x11AF + Mc, dev)
+            yh = torch.empty((Mc, N), dtype=torch.bfloat16, device=dev)
+            seq = [(cw[(li, name)].data_ptr(), xs[Kc].data_ptr(), ys[Nc].data_ptr(), Nc, Kc)
+                   for li, name, Nc, Kc in calls]
+            seq.append((packs[0].data_ptr(), xh.data_ptr(), yh.data_ptr(), N, K))
+
+            def traversal(seq=seq, Mc=Mc):
+                for pp, xx, yy, Nc, Kc in seq:
+                    lib.cudalm_w4a16_gemv_bf16_prepacked(pp, xx, yy, Nc, Kc, Mc, sraw)
+
+            t = graph_time(torch, traversal, 10, stream)
+            tot_bytes = sum(algo_bytes(Nc, Kc, Mc) for _, _, _, Nc, Kc in seq)
+            proj_bytes = sum(algo_bytes(Nc, Kc, Mc) for _, _, _, Nc, Kc in seq[:-1])
+            census[f"M{Mc}"] = {
+                "us_per_decode_step": round(t * 1e6, 2),
+                "calls": len(seq),
+                "bytes": tot_bytes,
+                "GBps": round(tot_bytes / t / 1e9, 1),
+                "frac_hbm_peak": round(tot_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                "projection_bytes_no_lm_head": proj_bytes,
+            }
+        extra["census"] = census
+        del cw
+
+    # ---------------- prefill chunk GEMM, M = 512 ----------------
+    if not args.no_prefill:
+        pre = {}
+        Mp = 512
+        for Np, Kp in ((3584, 1024), (1024, 3584), (6144, 1024), (4096, 1024), (2048, 1024),
+                       (1024, 2048), (512, 1024)):
+            w, s = synth_weights(torch, Np, Kp, 0xBEEF + Np + Kp, dev)
+            p = w4.repack(w, s, Np, Kp)
+            xpf = synth_act(torch, Mp, Kp, 0xF00D, dev)
+            ypf = torch.empty((Mp, Np), dtype=torch.bfloat16, device=dev)
+            pp, xx, yy = p.data_ptr(), xpf.data_ptr(), ypf.data_ptr()
+            t = graph_time(torch, lambda: [lib.cudalm_w4a16_gemv_bf16_prepacked(pp, xx, yy, Np, Kp, Mp, sraw)
+                                           for _ in range(10)], 5, stream) / 10
+            fl = 2.0 * Mp * Np * Kp
+            pre[f"{Np}x{Kp}"] = {"us": round(t * 1e6, 2), "TFLOPs": round(fl / t / 1e12, 1),
+                                 "frac_bf16_peak": round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 4)}
+        extra["prefill_M512"] = pre
+
+    # ---------------- CPU baseline (oracle restatement of ref_gemv_bf16) ----------------
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        Wn = ws[0].cpu().numpy()
+        Sn = ss[0].view(torch.int16).cpu().numpy().view(np.uint16)
+        Xn = x.view(torch.int16).cpu().numpy().view(np.uint16)
+        threads = min(oracle.hardware_threads(), 16)
+        one = oracle.time_gemv_bf16(Wn, Sn, Xn, N, K, 1, threads, 1)
+        iters = max(1, int(args.cpu_seconds / max(one, 1e-3)))
+        t_cpu = oracle.time_gemv_bf16(Wn, Sn, Xn, N, K, 1, threads, iters)
+        cpu = {"value": round(nbytes / t_cpu / 1e9, 2), "unit": "GB/s", "cores": threads,
+               "kind": "port",
+               "sample": f"full LM-head GEMV (N={N}, K={K}, M=1), {iters} calls after 1 warm-up, "
+                         f"rows split over {threads} threads; {t_cpu * 1e3:.1f} ms per call"}
+        # single-core form of the reference's loop, on a bounded row sample
+        rows = 16384
+        t1 = oracle.time_gemv_bf16(Wn[:rows].copy(), Sn[:rows].copy(), Xn, rows, K, 1, 1, 3)
+        cpu["single_core_GBps"] = round(algo_bytes(rows, K, 1) / t1 / 1e9, 3)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xbf16->fp32",
+        "data": "synthetic (torch-seeded N(0,0.02) weights quantized W4A16 G=128; N(0,1) bf16 x)",
+        "config": {"workload": "LM-head W4A16 GEMV, M=1, K=1024, N=248320 (BASELINE configs[1]), "
+                               "prepacked weights, 4 rotating copies",
+                   "M": M, "N": N, "K": K, "group": 128, "parallelism": "single-gpu"},
+        "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "w4a16_stream_kernel<true>",
+                     "kernel_us": round(per_launch * 1e6, 3),
+                     "algorithmic_bytes_per_launch": nbytes},
+        "file_layout_entry": {"kernel_us": round(file_per * 1e6, 3), "GBps": round(file_gbs, 1)},
+        "config0_M1_3584x1024": {"us": round(cfg0_s * 1e6, 3),
+                                 "GBps": round(algo_bytes(N0, K0, 1) / cfg0_s / 1e9, 1)},
+        "cpu_baseline": cpu,
+    }
+    out.update(extra)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
