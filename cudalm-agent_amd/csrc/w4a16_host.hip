@@ -94,29 +94,34 @@ extern "C" int cudalm_w4a16_repack_host(const uint8_t* weight, const uint16_t* s
                                         void* packed, int N, int K) {
   if (N < 1 || K <= 0 || K % CUDALM_W4A16_GROUP != 0) return CUDALM_W4A16_EINVAL;
   if (!weight || !scale || !packed) return CUDALM_W4A16_ENULL;
+  // Layout (the kernels' prepacked form): per 16-row tile, G groups of
+  // 1024 weight bytes (lane l = 16a + i: row i, bytes [16a, 16a+16) of the
+  // group), then 16 rows of scales with a pitch of 16 * ceil(G/8) bytes.
   const int G = K / CUDALM_W4A16_GROUP;
+  const int SP = 16 * ((G + 7) / 8);
+  const std::size_t tile_bytes = static_cast<std::size_t>(G) * 1024 + 16 * static_cast<std::size_t>(SP);
   const int ntiles = (N + 15) / 16;
   std::uint8_t* out = static_cast<std::uint8_t*>(packed);
-  const std::uint8_t* sb = reinterpret_cast<const std::uint8_t*>(scale);
   for (int rt = 0; rt < ntiles; ++rt) {
+    std::uint8_t* tile = out + static_cast<std::size_t>(rt) * tile_bytes;
     for (int g = 0; g < G; ++g) {
-      std::uint8_t* blk = out + (static_cast<std::size_t>(rt) * G + g) * 1056;
       for (int l = 0; l < 64; ++l) {
         const int n = rt * 16 + (l & 15);
         const int a = l >> 4;
+        std::uint8_t* dst = tile + static_cast<std::size_t>(g) * 1024 + 16 * l;
         if (n < N)
-          std::memcpy(blk + 16 * l, weight + static_cast<std::size_t>(n) * (K / 2) + g * 64 + a * 16,
-                      16);
+          std::memcpy(dst, weight + static_cast<std::size_t>(n) * (K / 2) + g * 64 + a * 16, 16);
         else
-          std::memset(blk + 16 * l, 0, 16);
+          std::memset(dst, 0, 16);
       }
-      for (int r = 0; r < 16; ++r) {
-        const int n = rt * 16 + r;
-        if (n < N)
-          std::memcpy(blk + 1024 + 2 * r, sb + (static_cast<std::size_t>(n) * G + g) * 2, 2);
-        else
-          std::memset(blk + 1024 + 2 * r, 0, 2);
-      }
+    }
+    std::uint8_t* srows = tile + static_cast<std::size_t>(G) * 1024;
+    std::memset(srows, 0, 16 * static_cast<std::size_t>(SP));
+    for (int r = 0; r < 16; ++r) {
+      const int n = rt * 16 + r;
+      if (n < N)
+        std::memcpy(srows + static_cast<std::size_t>(r) * SP,
+                    scale + static_cast<std::size_t>(n) * G, 2 * static_cast<std::size_t>(G));
     }
   }
   return CUDALM_W4A16_OK;

@@ -7,33 +7,45 @@
 //
 // How the contraction maps onto CDNA4 matrix cores
 // -------------------------------------------------
-// Every kernel below computes 16-row x 16-column output tiles with
-// v_mfma_f32_16x16x32_bf16 (A = weights, rows n; B = activations, columns m).
-// One 128-wide quantization group of one 16-row tile is a 1 KB slab of
-// packed weights: lane l = 16*a + i loads the 16 bytes of row i that hold
-// k = 32a .. 32a+31 of the group, and each of its four dwords feeds one MFMA
-// step (8 k per lane per step, 32 k per step).
+// Every kernel computes 16 x 16 output tiles (16 activation rows m x 16
+// weight rows n) with v_mfma_f32_16x16x32_bf16, activations as the A
+// operand and weights as the B operand. One 128-wide quantization group of
+// one 16-row weight tile is a 1 KB slab: lane l = 16a + i holds the 16
+// bytes of weight row i that carry k = 32a .. 32a+31 of the group, and each
+// of its four dwords feeds one MFMA step (8 k per lane, 32 k per step).
+// The lane's activation operand is row i, the same 32 k. After the four
+// steps lane l holds the group partial for rows m = 4a .. 4a+3 of column
+// n = i, so every lane applies exactly one fp16 group scale.
 //
-// A weight nibble n (two's complement q) is turned into an exact bf16 by
-// bit placement alone: bits 0x3F80 | ((n ^ 8) << 3) encode 1 + (q+8)/16 =
-// 1.5 + q/16. Two nibbles 16 bits apart become one bf16 pair with a shift
-// and one v_bitop3, so a dword of 8 nibbles costs 8 VALU ops. The constant
-// 1.5 is removed per group and column:
-//     sum_k q x = 16 * ( sum_k (1.5 + q/16) x  -  1.5 * sum_k x )
-// and the fp16 scale is applied once per group in fp32:
-//     acc = fma(s[n,g], tmp[n,m,g] - c[m,g], acc),   c[m,g] = 1.5 * sum_{k in g} x[m,k]
-// with the final y = bf16_rne(16 * acc). The pair layout the bit placement
-// produces is (k, k+4) for k = 0..3 of every 8-k block, so activations are
-// stored in LDS in that order: [x0 x4 x1 x5 x2 x6 x3 x7].
+// A weight nibble n (two's complement q) becomes an exact bf16 by bit
+// placement: 0x3F80 | ((n ^ 8) << 3) encodes 1 + (q+8)/16 = 1.5 + q/16.
+// Two nibbles 16 bits apart become one bf16 pair with one shift and one
+// v_bitop3 (8 VALU ops per dword of 8 weights). The constant is removed
+// inside the matrix core: a four-step MFMA chain against a constant -1.5
+// operand produces -1.5 * sum(x) per row and group, and it seeds the
+// accumulator of the weight chain, so
+//     tmp = -1.5 * sum_k x  +  sum_k (1.5 + q/16) x  =  (1/16) sum_k q x
+// and the per-group epilogue is one fma: acc = fma(s[n,g], tmp, acc); the
+// output is bf16_rne(16 * acc). The pair layout produced by the decoder is
+// (k, k+4) for k = 0..3 of each 8-k block, so activations sit in LDS in
+// that order: [x0 x4 x1 x5 x2 x6 x3 x7].
 //
-// Every kernel uses the same per-element operation sequence (same MFMA
-// operands, same group order, same epilogue), so one output element has the
-// same bits whichever kernel, tile shape, batch size or weight layout
-// produced it. The tests pin that.
+// All kernels run the same per-output operation sequence (same MFMA
+// operands in the same slots, same chains, same group order, same
+// epilogue), so an output has the same bits whichever kernel, tile shape,
+// batch size or weight layout produced it. The tests pin that.
+//
+// Prepacked ("repacked at load") weight layout, per 16-row tile:
+//   [G x 1024 B weights: group g at g*1024, lane l's 16 bytes at 16*l]
+//   [16 rows x SP B scales: row i at G*1024 + i*SP, fp16 of groups 0..G-1,
+//    SP = 16 * ceil(G/8) (zero padded)]
+// so one wave load of a group is 1 KB contiguous and one 16-byte load
+// brings a lane the scales of 8 consecutive groups. Rows >= N are zero.
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "cudalm_w4a16.h"
 
@@ -42,27 +54,30 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kGroup = 128;          // quantization group (k)
-constexpr int kTileRows = 16;        // output rows per MFMA tile
-constexpr int kPackedBlock = 1056;   // prepacked bytes per (16-row tile, group)
-constexpr int kPackedScaleOff = 1024;
+constexpr int kGroup = 128;     // quantization group (k)
+constexpr int kTileRows = 16;   // weight rows per MFMA tile
+constexpr int kUnit = 8;        // groups per streamed unit
+constexpr uint32_t kNegOffsetPair = 0xBFC0BFC0u;  // bf16 -1.5 in both halves
+
+__host__ __device__ constexpr int packed_scale_pitch(int G) { return 16 * ((G + 7) / 8); }
+__host__ __device__ constexpr size_t packed_tile_bytes(int G) {
+  return static_cast<size_t>(G) * 1024 + 16 * static_cast<size_t>(packed_scale_pitch(G));
+}
 
 // ---------------------------------------------------------------------------
 // device helpers
 // ---------------------------------------------------------------------------
 
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+}
+
 __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
 }
 
-__device__ __forceinline__ float bf16_lo(uint32_t v) {
-  return __builtin_bit_cast(float, v << 16);
-}
-__device__ __forceinline__ float bf16_hi(uint32_t v) {
-  return __builtin_bit_cast(float, v & 0xFFFF0000u);
-}
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }
 
 // fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
@@ -94,167 +109,129 @@ __device__ __forceinline__ u32x4_t pair_order(u32x4_t v) {
 
 __device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                 __builtin_bit_cast(bf16x8_t, b), c,
-                                                 0, 0, 0);
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// 1.5 * (sum of the 128 activations of one group), summed in LDS storage
-// order (16 blocks ascending, pairs ascending, low element first).
-__device__ __forceinline__ float group_offset(const u32x4_t* blocks) {
-  float s = 0.0f;
-#pragma unroll
-  for (int b = 0; b < 16; ++b) {
-    const u32x4_t v = blocks[b];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      s += bf16_lo(v[r]);
-      s += bf16_hi(v[r]);
-    }
-  }
-  return 1.5f * s;
-}
-
-// One group of one 16x16 tile: four MFMA steps over the lane's 16 weight
-// bytes. xrow points at the lane's LDS activation row, at the group start.
-__device__ __forceinline__ f32x4_t group_product(u32x4_t w, const u32x4_t* xgroup,
-                                                 int a) {
+// -1.5 * (sum over the group of this lane-set's activation rows), as a 16x16
+// accumulator tile (all columns equal).
+__device__ __forceinline__ f32x4_t group_offset(const u32x4_t (&xa)[4]) {
+  const u32x4_t neg = {kNegOffsetPair, kNegOffsetPair, kNegOffsetPair, kNegOffsetPair};
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f32x4_t t = mfma16(decode_nibbles(w[0]), xgroup[4 * a + 0], zero);
-  t = mfma16(decode_nibbles(w[1]), xgroup[4 * a + 1], t);
-  t = mfma16(decode_nibbles(w[2]), xgroup[4 * a + 2], t);
-  t = mfma16(decode_nibbles(w[3]), xgroup[4 * a + 3], t);
+  f32x4_t c = mfma16(xa[0], neg, zero);
+  c = mfma16(xa[1], neg, c);
+  c = mfma16(xa[2], neg, c);
+  c = mfma16(xa[3], neg, c);
+  return c;
+}
+
+// (1/16) sum_k q x over one group of one 16x16 tile.
+__device__ __forceinline__ f32x4_t group_product(u32x4_t w, const u32x4_t (&xa)[4], f32x4_t corr) {
+  f32x4_t t = mfma16(xa[0], decode_nibbles(w[0]), corr);
+  t = mfma16(xa[1], decode_nibbles(w[1]), t);
+  t = mfma16(xa[2], decode_nibbles(w[2]), t);
+  t = mfma16(xa[3], decode_nibbles(w[3]), t);
   return t;
 }
 
-__device__ __forceinline__ void group_epilogue(f32x4_t& acc, f32x4_t t, float c,
-                                               const float (&s)[4]) {
+__device__ __forceinline__ void load_group_x(u32x4_t (&xa)[4], const u32x4_t* xgroup, int a) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(s[r], t[r] - c, acc[r]);
+  for (int d = 0; d < 4; ++d) xa[d] = xgroup[4 * a + d];
 }
 
-__device__ __forceinline__ void scales_from_u32x2(u32x2_t v, float (&s)[4]) {
-  s[0] = half_bits_to_f32(v[0] & 0xFFFFu);
-  s[1] = half_bits_to_f32(v[0] >> 16);
-  s[2] = half_bits_to_f32(v[1] & 0xFFFFu);
-  s[3] = half_bits_to_f32(v[1] >> 16);
-}
-
-// Store one lane's four outputs (rows n0..n0+3 of column m).
-__device__ __forceinline__ void store_tile_column(uint16_t* __restrict__ Y, f32x4_t acc,
-                                                  size_t ybase, int n0, int N) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    if (n0 + r < N) Y[ybase + n0 + r] = static_cast<uint16_t>(f32_to_bf16_rne(16.0f * acc[r]));
-  }
+// scale of group gg (0..7) from 8 packed fp16
+__device__ __forceinline__ float unit_scale(u32x4_t sv, int gg) {
+  return half_bits_to_f32((sv[gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
 }
 
 // Stage rows [m0, m0+mrows) x k [k0, k0+kcl) of X into LDS in pair order,
 // row pitch `pitch` 16-byte blocks.
 __device__ __forceinline__ void stage_activations(u32x4_t* xs, int pitch,
-                                                  const uint16_t* __restrict__ X,
-                                                  int K, int m0, int mrows, int k0,
-                                                  int kcl) {
+                                                  const uint16_t* __restrict__ X, int K, int m0,
+                                                  int mrows, int k0, int kcl) {
   const int nb = kcl >> 3;
   for (int t = threadIdx.x; t < mrows * nb; t += blockDim.x) {
     const int mm = t / nb;
     const int b = t - mm * nb;
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(
-        X + static_cast<size_t>(m0 + mm) * K + k0 + 8 * b);
+    const u32x4_t v =
+        *reinterpret_cast<const u32x4_t*>(X + static_cast<size_t>(m0 + mm) * K + k0 + 8 * b);
     xs[mm * pitch + b] = pair_order(v);
-  }
-}
-
-__device__ __forceinline__ void stage_offsets(float* cs, int cpitch, const u32x4_t* xs,
-                                              int pitch, int mrows, int ng) {
-  for (int t = threadIdx.x; t < mrows * ng; t += blockDim.x) {
-    const int mm = t / ng;
-    const int gl = t - mm * ng;
-    cs[mm * cpitch + gl] = group_offset(xs + mm * pitch + gl * 16);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Stream kernel: M <= 16, all of x resident in LDS, waves stream 16-row
-// tiles (grid-stride), prefetching the next unit of up to 8 groups while
-// the current one is computed.
+// weight tiles (grid-stride) in units of up to 8 groups, prefetching the
+// next unit while the current one is multiplied. NR = accumulator rows per
+// lane that can hold outputs (1 when M == 1, else 4).
 // ---------------------------------------------------------------------------
 
 constexpr int kStreamWaves = 4;
-constexpr int kStreamUnit = 8;  // groups per unit
 
-template <bool PACKED>
 struct StreamUnit {
-  u32x4_t w[kStreamUnit];
-  u32x2_t s[kStreamUnit];  // PACKED: this lane's 4 row scales per group
-  uint32_t s0, s1;         // file layout: two raw scales this lane stages
+  u32x4_t w[kUnit];
+  u32x4_t s;  // fp16 scales of the unit's 8 groups for this lane's weight row
 };
 
-template <bool PACKED>
-__device__ __forceinline__ void stream_load(StreamUnit<PACKED>& u,
-                                            const uint8_t* __restrict__ W,
-                                            const uint16_t* __restrict__ S, int N,
-                                            int K, int G, int rt, int g0, int gn,
-                                            int lane) {
+// Loads are unconditional (group indices clamped to G-1) so the compiler's
+// memory counters see one straight-line batch per unit and the compute of
+// the current unit waits only for its own data.
+template <bool PACKED, bool SVEC>
+__device__ __forceinline__ void stream_load(StreamUnit& u, const uint8_t* __restrict__ W,
+                                            const uint16_t* __restrict__ S, int N, int K, int G,
+                                            int rt, int g0, int lane) {
+  const int i = lane & 15, a = lane >> 4;
   if constexpr (PACKED) {
-    const uint8_t* base = W + (static_cast<size_t>(rt) * G + g0) * kPackedBlock;
+    const uint8_t* tile = W + static_cast<size_t>(rt) * packed_tile_bytes(G);
 #pragma unroll
-    for (int gg = 0; gg < kStreamUnit; ++gg) {
-      if (gg < gn) {
-        u.w[gg] = *reinterpret_cast<const u32x4_t*>(base + gg * kPackedBlock + lane * 16);
-        u.s[gg] = *reinterpret_cast<const u32x2_t*>(base + gg * kPackedBlock +
-                                                    kPackedScaleOff + (lane >> 4) * 8);
-      }
-    }
+    for (int gg = 0; gg < kUnit; ++gg)
+      u.w[gg] = *reinterpret_cast<const u32x4_t*>(tile + min(g0 + gg, G - 1) * 1024 + lane * 16);
+    u.s = *reinterpret_cast<const u32x4_t*>(tile + static_cast<size_t>(G) * 1024 +
+                                            i * packed_scale_pitch(G) + 2 * g0);
   } else {
-    const int i = lane & 15, a = lane >> 4;
     const int row = min(rt * kTileRows + i, N - 1);
     const uint8_t* wrow = W + static_cast<size_t>(row) * (K >> 1) + a * 16;
 #pragma unroll
-    for (int gg = 0; gg < kStreamUnit; ++gg) {
-      if (gg < gn) u.w[gg] = *reinterpret_cast<const u32x4_t*>(wrow + (g0 + gg) * 64);
+    for (int gg = 0; gg < kUnit; ++gg)
+      u.w[gg] = *reinterpret_cast<const u32x4_t*>(wrow + min(g0 + gg, G - 1) * 64);
+    const uint16_t* srow = S + static_cast<size_t>(row) * G;
+    if constexpr (SVEC) {
+      u.s = *reinterpret_cast<const u32x4_t*>(srow + g0);
+    } else {
+      uint32_t h[kUnit];
+#pragma unroll
+      for (int gg = 0; gg < kUnit; ++gg) h[gg] = srow[min(g0 + gg, G - 1)];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) u.s[q] = h[2 * q] | (h[2 * q + 1] << 16);
     }
-    const int srow = min(rt * kTileRows + (lane >> 2), N - 1);
-    const int gq = 2 * (lane & 3);
-    const uint16_t* sp = S + static_cast<size_t>(srow) * G + g0 + gq;
-    u.s0 = (gq < gn) ? sp[0] : 0u;
-    u.s1 = (gq + 1 < gn) ? sp[1] : 0u;
   }
 }
 
-template <bool PACKED>
+template <bool PACKED, int NR, bool SVEC>
 __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
     const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
     const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, int N, int K, int M) {
-  extern __shared__ u32x4_t smem[];
+  extern __shared__ u32x4_t xs[];
   const int G = K >> 7;
   const int pitch = (K >> 3) + 1;
-  u32x4_t* xs = smem;
-  float* cs = reinterpret_cast<float*>(smem + M * pitch);
-  uint16_t* ss = reinterpret_cast<uint16_t*>(cs + ((M * G + 3) & ~3));
-
-  stage_activations(xs, pitch, X, K, 0, M, 0, K);
-  __syncthreads();
-  stage_offsets(cs, G, xs, pitch, M, G);
-  __syncthreads();
-
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int i = lane & 15, a = lane >> 4;
-  const int col = min(i, M - 1);
-  const u32x4_t* xrow = xs + col * pitch;
-  const float* crow = cs + col * G;
-  uint16_t* wss = ss + wave * (kStreamUnit * kTileRows);
-
   const int ntiles = (N + kTileRows - 1) / kTileRows;
-  const int U = (G + kStreamUnit - 1) / kStreamUnit;
+  const int U = (G + kUnit - 1) / kUnit;
   const int stride = gridDim.x * kStreamWaves;
   int t = blockIdx.x * kStreamWaves + wave;
-  if (t >= ntiles) return;
-  int u = 0;
+  const bool active = t < ntiles;
 
-  StreamUnit<PACKED> cur, nxt;
-  stream_load<PACKED>(cur, W, S, N, K, G, t, 0, min(kStreamUnit, G), lane);
+  // first unit's weights fly while the activations are staged
+  StreamUnit cur, nxt;
+  stream_load<PACKED, SVEC>(cur, W, S, N, K, G, min(t, ntiles - 1), 0, lane);
+  stage_activations(xs, pitch, X, K, 0, M, 0, K);
+  __syncthreads();
+  if (!active) return;
+
+  const u32x4_t* xrow = xs + min(i, M - 1) * pitch;
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  int u = 0;
   while (true) {
     int nt = t, nu = u + 1;
     if (nu == U) {
@@ -262,35 +239,31 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
       nt = t + stride;
     }
     const bool has_next = nt < ntiles;
-    if (has_next)
-      stream_load<PACKED>(nxt, W, S, N, K, G, nt, nu * kStreamUnit,
-                          min(kStreamUnit, G - nu * kStreamUnit), lane);
-
-    const int g0 = u * kStreamUnit;
-    const int gn = min(kStreamUnit, G - g0);
-    if constexpr (!PACKED) {
-      // transpose this unit's scales to [group][row] so each lane reads its
-      // four rows of one group with one 8-byte LDS load
-      const int gq = 2 * (lane & 3);
-      wss[gq * kTileRows + (lane >> 2)] = static_cast<uint16_t>(cur.s0);
-      wss[(gq + 1) * kTileRows + (lane >> 2)] = static_cast<uint16_t>(cur.s1);
-    }
+    // past the last unit, re-read the current one (cache hits) instead of
+    // branching around the loads
+    stream_load<PACKED, SVEC>(nxt, W, S, N, K, G, has_next ? nt : t, has_next ? nu * kUnit : u * kUnit,
+                              lane);
+    const int g0 = u * kUnit;
+    const int gn = min(kUnit, G - g0);
 #pragma unroll
-    for (int gg = 0; gg < kStreamUnit; ++gg) {
+    for (int gg = 0; gg < kUnit; ++gg) {
       if (gg < gn) {
-        const int g = g0 + gg;
-        const f32x4_t tp = group_product(cur.w[gg], xrow + g * 16, a);
-        float s[4];
-        if constexpr (PACKED) {
-          scales_from_u32x2(cur.s[gg], s);
-        } else {
-          scales_from_u32x2(*reinterpret_cast<const u32x2_t*>(wss + gg * kTileRows + 4 * a), s);
-        }
-        group_epilogue(acc, tp, crow[g], s);
+        u32x4_t xa[4];
+        load_group_x(xa, xrow + (g0 + gg) * 16, a);
+        const f32x4_t tp = group_product(cur.w[gg], xa, group_offset(xa));
+        const float s = unit_scale(cur.s, gg);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) acc[r] = __builtin_fmaf(s, tp[r], acc[r]);
       }
     }
     if (u == U - 1) {
-      if (i < M) store_tile_column(Y, acc, static_cast<size_t>(i) * N, t * kTileRows + 4 * a, N);
+      const int n = t * kTileRows + i;
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int m = 4 * a + r;
+        if (m < M && n < N)
+          Y[static_cast<size_t>(m) * N + n] = static_cast<uint16_t>(f32_to_bf16_rne(16.0f * acc[r]));
+      }
       acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
     if (!has_next) break;
@@ -302,7 +275,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
 
 // ---------------------------------------------------------------------------
 // Tile kernel: any M. A workgroup of WN x WM waves owns a (WN*RB*16) x
-// (WM*CT*16) output tile; K is walked in chunks of GPC groups whose
+// (WM*CT*16) output tile (n x m); K is walked in chunks of GPC groups whose
 // activations are staged in LDS; each wave preloads the chunk's weights.
 // ---------------------------------------------------------------------------
 
@@ -310,20 +283,18 @@ template <int RB, int CT, int WN, int WM, int GPC, bool PACKED>
 __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
     const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
     const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, int N, int K, int M) {
-  extern __shared__ u32x4_t smem[];
+  extern __shared__ u32x4_t xs[];
   constexpr int CM = WM * CT * 16;
   constexpr int KC = GPC * kGroup;
   constexpr int pitch = KC / 8 + 1;
   const int G = K >> 7;
   const int ntiles = (N + kTileRows - 1) / kTileRows;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int wn = wave % WN, wm = wave / WN;
   const int i = lane & 15, a = lane >> 4;
   const int m0 = blockIdx.y * CM;
   const int mrows = min(CM, M - m0);
-  u32x4_t* xs = smem;
-  float* cs = reinterpret_cast<float*>(smem + mrows * pitch);
 
   int rt[RB];
   bool rt_ok[RB];
@@ -333,9 +304,9 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
     rt_ok[rb] = r < ntiles;
     rt[rb] = min(r, ntiles - 1);
   }
-  int colv[CT];
+  int xr[CT];
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) colv[ct] = min(wm * CT * 16 + ct * 16 + i, mrows - 1);
+  for (int ct = 0; ct < CT; ++ct) xr[ct] = min(wm * CT * 16 + ct * 16 + i, mrows - 1) * pitch;
 
   f32x4_t acc[RB][CT];
 #pragma unroll
@@ -345,9 +316,9 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
 
   for (int g0 = 0; g0 < G; g0 += GPC) {
     const int ng = min(GPC, G - g0);
-    // issue this chunk's weight and scale loads first; they fly during staging
+    // this chunk's weight and scale loads fly during staging
     u32x4_t w[GPC][RB];
-    float s[GPC][RB][4];
+    float s[GPC][RB];
 #pragma unroll
     for (int gl = 0; gl < GPC; ++gl) {
       if (gl < ng) {
@@ -355,53 +326,51 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
           if constexpr (PACKED) {
-            const uint8_t* blk = W + (static_cast<size_t>(rt[rb]) * G + g) * kPackedBlock;
-            w[gl][rb] = *reinterpret_cast<const u32x4_t*>(blk + lane * 16);
-            scales_from_u32x2(*reinterpret_cast<const u32x2_t*>(blk + kPackedScaleOff + a * 8),
-                              s[gl][rb]);
+            const uint8_t* tile = W + static_cast<size_t>(rt[rb]) * packed_tile_bytes(G);
+            w[gl][rb] = *reinterpret_cast<const u32x4_t*>(tile + g * 1024 + lane * 16);
+            s[gl][rb] = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(
+                tile + static_cast<size_t>(G) * 1024 + i * packed_scale_pitch(G) + 2 * g));
           } else {
             const int row = min(rt[rb] * kTileRows + i, N - 1);
             w[gl][rb] = *reinterpret_cast<const u32x4_t*>(
                 W + static_cast<size_t>(row) * (K >> 1) + g * 64 + a * 16);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int srow = min(rt[rb] * kTileRows + 4 * a + r, N - 1);
-              s[gl][rb][r] = half_bits_to_f32(S[static_cast<size_t>(srow) * G + g]);
-            }
+            s[gl][rb] = half_bits_to_f32(S[static_cast<size_t>(row) * G + g]);
           }
         }
       }
     }
-    __syncthreads();  // previous chunk's LDS reads are done
+    __syncthreads();  // the previous chunk's LDS reads are done
     stage_activations(xs, pitch, X, K, m0, mrows, g0 * kGroup, ng * kGroup);
-    __syncthreads();
-    stage_offsets(cs, GPC, xs, pitch, mrows, ng);
     __syncthreads();
 
 #pragma unroll
     for (int gl = 0; gl < GPC; ++gl) {
       if (gl < ng) {
+        u32x4_t xa[CT][4];
         f32x4_t tp[RB][CT];
-        const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          load_group_x(xa[ct], xs + xr[ct] + gl * 16, a);
+          const f32x4_t corr = group_offset(xa[ct]);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) tp[rb][ct] = corr;
+        }
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-          u32x4_t A[RB];
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb) A[rb] = decode_nibbles(w[gl][rb][d]);
+          for (int rb = 0; rb < RB; ++rb) {
+            const u32x4_t B = decode_nibbles(w[gl][rb][d]);
 #pragma unroll
-          for (int ct = 0; ct < CT; ++ct) {
-            const u32x4_t B = xs[colv[ct] * pitch + gl * 16 + 4 * a + d];
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
-              tp[rb][ct] = mfma16(A[rb], B, d == 0 ? zero : tp[rb][ct]);
+            for (int ct = 0; ct < CT; ++ct) tp[rb][ct] = mfma16(xa[ct][d], B, tp[rb][ct]);
           }
         }
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          const float c = cs[colv[ct] * GPC + gl];
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb) group_epilogue(acc[rb][ct], tp[rb][ct], c, s[gl][rb]);
-        }
+          for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[rb][ct][r] = __builtin_fmaf(s[gl][rb], tp[rb][ct][r], acc[rb][ct][r]);
       }
     }
   }
@@ -409,13 +378,17 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     if (!rt_ok[rb]) continue;
+    const int n = rt[rb] * kTileRows + i;
+    if (n >= N) continue;
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      const int cl = wm * CT * 16 + ct * 16 + i;
-      if (cl < mrows)
-        store_tile_column(Y, acc[rb][ct], static_cast<size_t>(m0 + cl) * N,
-                          rt[rb] * kTileRows + 4 * a, N);
-    }
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ml = wm * CT * 16 + ct * 16 + 4 * a + r;
+        if (ml < mrows)
+          Y[static_cast<size_t>(m0 + ml) * N + n] =
+              static_cast<uint16_t>(f32_to_bf16_rne(16.0f * acc[rb][ct][r]));
+      }
   }
 }
 
@@ -433,7 +406,7 @@ __global__ __launch_bounds__(256) void w4a16_bytewise_kernel(
     const uint8_t* __restrict__ W, const uint8_t* __restrict__ Sb,
     const uint8_t* __restrict__ Xb, uint8_t* __restrict__ Yb, int N, int K) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * 4 + wave_id();
   const int m = blockIdx.y;
   if (row >= N) return;
   const int G = K >> 7;
@@ -479,8 +452,8 @@ __global__ __launch_bounds__(256) void w4a16_dequant_kernel(
   const size_t k0 = n * K + dw * 8;
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const float e0 = (bf16_lo(pairs[p]) - 1.5f) * 16.0f;  // element k0 + p
-    const float e1 = (bf16_hi(pairs[p]) - 1.5f) * 16.0f;  // element k0 + p + 4
+    const float e0 = (bf16_lo(pairs[p]) - 1.5f) * 16.0f;               // element k0 + p
+    const float e1 = (bf16_lo(pairs[p] >> 16) - 1.5f) * 16.0f;         // element k0 + p + 4
     if (qo) {
       qo[k0 + p] = static_cast<int8_t>(e0);
       qo[k0 + p + 4] = static_cast<int8_t>(e1);
@@ -493,37 +466,38 @@ __global__ __launch_bounds__(256) void w4a16_dequant_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Load-time repack: file layout -> tile-major blocks of 1056 bytes per
-// (16-row tile, group): bytes [16l, 16l+16) hold row l%16, k-bytes
-// [16(l/16), +16) of the group (what MFMA lane l loads); bytes [1024, 1056)
-// hold the group's 16 row scales (fp16) in row order. Rows >= N are zero.
+// Load-time repack: file layout -> prepacked tiles (layout at the top of the
+// file). One thread per 16-byte unit of the output.
 // ---------------------------------------------------------------------------
 
 __global__ __launch_bounds__(256) void w4a16_repack_kernel(
-    const uint8_t* __restrict__ W, const uint8_t* __restrict__ Sb,
-    uint8_t* __restrict__ P, int N, int K) {
+    const uint8_t* __restrict__ W, const uint8_t* __restrict__ Sb, uint8_t* __restrict__ P, int N,
+    int K) {
   const int G = K >> 7;
-  const size_t units_per_block = kPackedBlock / 16;  // 66
-  const size_t nunits = static_cast<size_t>((N + 15) / 16) * G * units_per_block;
+  const int SP = packed_scale_pitch(G);
+  const size_t units_per_tile = packed_tile_bytes(G) / 16;
+  const size_t nunits = static_cast<size_t>((N + 15) / 16) * units_per_tile;
   const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= nunits) return;
-  const size_t blk = idx / units_per_block;
-  const int j = static_cast<int>(idx - blk * units_per_block);
-  const int rt = static_cast<int>(blk / G);
-  const int g = static_cast<int>(blk - static_cast<size_t>(rt) * G);
+  const int rt = static_cast<int>(idx / units_per_tile);
+  const int j = static_cast<int>(idx - static_cast<size_t>(rt) * units_per_tile);
   uint8_t out[16];
-  if (j < 64) {
-    const int n = rt * 16 + (j & 15);
-    const int a = j >> 4;
+  if (j < G * 64) {
+    const int g = j >> 6, l = j & 63;
+    const int n = rt * 16 + (l & 15);
+    const int a = l >> 4;
     for (int b = 0; b < 16; ++b)
       out[b] = (n < N) ? W[static_cast<size_t>(n) * (K >> 1) + g * 64 + a * 16 + b] : 0;
   } else {
-    const int r0 = (j - 64) * 8;
-    for (int r = 0; r < 8; ++r) {
-      const int n = rt * 16 + r0 + r;
+    const int jj = j - G * 64;
+    const int row = jj / (SP / 16), u = jj - row * (SP / 16);
+    const int n = rt * 16 + row;
+    for (int q = 0; q < 8; ++q) {
+      const int g = 8 * u + q;
+      const bool ok = n < N && g < G;
       const size_t so = (static_cast<size_t>(n) * G + g) * 2;
-      out[2 * r] = (n < N) ? Sb[so] : 0;
-      out[2 * r + 1] = (n < N) ? Sb[so + 1] : 0;
+      out[2 * q] = ok ? Sb[so] : 0;
+      out[2 * q + 1] = ok ? Sb[so + 1] : 0;
     }
   }
   u32x4_t v;
@@ -538,7 +512,7 @@ __global__ __launch_bounds__(256) void w4a16_repack_kernel(
 // host launch layer
 // ---------------------------------------------------------------------------
 
-constexpr size_t kLdsBudget = 64 * 1024;
+constexpr size_t kStreamLdsBudget = 64 * 1024;
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
@@ -569,40 +543,80 @@ int launch_status() {
   return e == hipSuccess ? CUDALM_W4A16_OK : CUDALM_W4A16_ELAUNCH;
 }
 
-size_t stream_lds_bytes(int K, int M) {
-  const int G = K / kGroup;
-  const size_t x = static_cast<size_t>(M) * (K / 8 + 1) * 16;
-  const size_t c = static_cast<size_t>((M * G + 3) & ~3) * 4;
-  const size_t s = static_cast<size_t>(kStreamWaves) * kStreamUnit * kTileRows * 2;
-  return x + c + s;
+// Dynamic LDS above 64 KB must be opted into once per kernel.
+template <typename F>
+bool allow_lds(F kernel, size_t bytes) {
+  if (bytes <= 64 * 1024) return true;
+  static thread_local const void* done[64] = {nullptr};
+  for (auto& d : done) {
+    if (d == reinterpret_cast<const void*>(kernel)) return true;
+    if (d == nullptr) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(bytes > 160 * 1024 ? bytes : 160 * 1024)) != hipSuccess)
+        return false;
+      d = reinterpret_cast<const void*>(kernel);
+      return true;
+    }
+  }
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+}
+
+size_t stream_lds_bytes(int K, int M) { return static_cast<size_t>(M) * (K / 8 + 1) * 16; }
+
+int stream_occupancy() {
+  static int occ = 0;
+  if (occ == 0) {
+    int v = 4;
+    if (const char* e = getenv("CUDALM_W4A16_STREAM_WGS_PER_CU")) {
+      const int p = atoi(e);
+      if (p >= 1 && p <= 32) v = p;
+    }
+    occ = v;
+  }
+  return occ;
+}
+
+template <bool PACKED, int NR, bool SVEC>
+int launch_stream_t(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
+                    int K, int M, hipStream_t stream) {
+  const size_t lds = stream_lds_bytes(K, M);
+  const int ntiles = (N + kTileRows - 1) / kTileRows;
+  const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
+  const int cap = cu_count() * stream_occupancy();
+  const int grid = want < cap ? want : cap;
+  hipLaunchKernelGGL((w4a16_stream_kernel<PACKED, NR, SVEC>), dim3(grid), dim3(kStreamWaves * 64),
+                     lds, stream, W, S, X, Y, N, K, M);
+  return launch_status();
 }
 
 template <bool PACKED>
 int launch_stream(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                   int K, int M, hipStream_t stream) {
-  const size_t lds = stream_lds_bytes(K, M);
-  const int ntiles = (N + kTileRows - 1) / kTileRows;
-  const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
-  const int cap = cu_count() * 4;
-  const int grid = want < cap ? want : cap;
-  hipLaunchKernelGGL(w4a16_stream_kernel<PACKED>, dim3(grid), dim3(kStreamWaves * 64), lds,
-                     stream, W, S, X, Y, N, K, M);
-  return launch_status();
+  const int G = K / kGroup;
+  const bool svec = !PACKED && (G % 8 == 0) && aligned(S, 16);
+  if (M == 1)
+    return svec ? launch_stream_t<PACKED, 1, true>(W, S, X, Y, N, K, M, stream)
+                : launch_stream_t<PACKED, 1, false>(W, S, X, Y, N, K, M, stream);
+  return svec ? launch_stream_t<PACKED, 4, true>(W, S, X, Y, N, K, M, stream)
+              : launch_stream_t<PACKED, 4, false>(W, S, X, Y, N, K, M, stream);
 }
 
 template <int RB, int CT, int WN, int WM, int GPC, bool PACKED>
-int launch_tile(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
-                int K, int M, hipStream_t stream) {
+int launch_tile(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N, int K,
+                int M, hipStream_t stream) {
   constexpr int CM = WM * CT * 16;
   constexpr int KC = GPC * kGroup;
   const int mrows = M < CM ? M : CM;
-  const size_t lds = static_cast<size_t>(mrows) * (KC / 8 + 1) * 16 + static_cast<size_t>(mrows) * GPC * 4;
+  const size_t lds = static_cast<size_t>(mrows) * (KC / 8 + 1) * 16;
   const int ntiles = (N + kTileRows - 1) / kTileRows;
   const int gx = (ntiles + WN * RB - 1) / (WN * RB);
   const int gy = (M + CM - 1) / CM;
   if (gy > 65535) return CUDALM_W4A16_ERANGE;
-  hipLaunchKernelGGL((w4a16_tile_kernel<RB, CT, WN, WM, GPC, PACKED>), dim3(gx, gy),
-                     dim3(WN * WM * 64), lds, stream, W, S, X, Y, N, K, M);
+  auto kern = w4a16_tile_kernel<RB, CT, WN, WM, GPC, PACKED>;
+  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+  hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(WN * WM * 64), lds, stream, W, S, X, Y, N, K, M);
   return launch_status();
 }
 
@@ -615,11 +629,13 @@ int launch_bytewise(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint
   return launch_status();
 }
 
+bool stream_fits(int K, int M) { return M <= 16 && stream_lds_bytes(K, M) <= kStreamLdsBudget; }
+
 template <bool PACKED>
 int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N, int K,
              int M, int variant, hipStream_t stream) {
   if (variant == CUDALM_W4A16_VARIANT_AUTO) {
-    if (M <= 16 && stream_lds_bytes(K, M) <= kLdsBudget)
+    if (stream_fits(K, M))
       variant = CUDALM_W4A16_VARIANT_STREAM;
     else if (M <= 16)
       variant = CUDALM_W4A16_VARIANT_TILE16;
@@ -630,14 +646,14 @@ int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y
   }
   switch (variant) {
     case CUDALM_W4A16_VARIANT_STREAM:
-      if (M > 16 || stream_lds_bytes(K, M) > kLdsBudget) return CUDALM_W4A16_EINVAL;
+      if (!stream_fits(K, M)) return CUDALM_W4A16_EVARIANT;
       return launch_stream<PACKED>(W, S, X, Y, N, K, M, stream);
     case CUDALM_W4A16_VARIANT_TILE16:
       return launch_tile<1, 1, 4, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
     case CUDALM_W4A16_VARIANT_TILE32:
       return launch_tile<1, 2, 4, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
     case CUDALM_W4A16_VARIANT_PREFILL:
-      return launch_tile<4, 4, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
+      return launch_tile<2, 4, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
     case CUDALM_W4A16_VARIANT_BYTEWISE:
       if (PACKED) return CUDALM_W4A16_EVARIANT;
       return launch_bytewise(W, S, X, Y, N, K, M, stream);
@@ -657,7 +673,7 @@ int regs_of(F kernel) {
 
 extern "C" {
 
-int cudalm_w4a16_version(void) { return 100; }
+int cudalm_w4a16_version(void) { return 200; }
 
 const char* cudalm_w4a16_strerror(int code) {
   switch (code) {
@@ -672,9 +688,9 @@ const char* cudalm_w4a16_strerror(int code) {
   }
 }
 
-int cudalm_w4a16_gemv_bf16_variant(const uint8_t* weight, const uint16_t* scale,
-                                   const uint16_t* x, uint16_t* y, int N, int K, int M,
-                                   int variant, hipStream_t stream) {
+int cudalm_w4a16_gemv_bf16_variant(const uint8_t* weight, const uint16_t* scale, const uint16_t* x,
+                                   uint16_t* y, int N, int K, int M, int variant,
+                                   hipStream_t stream) {
   if (int rc = check_shape(N, K, M)) return rc;
   if (!weight || !scale || !x || !y) return CUDALM_W4A16_ENULL;
   // The vectorized kernels need 16 B aligned weight rows and activation rows
@@ -697,7 +713,7 @@ int cudalm_w4a16_gemv_bf16(const uint8_t* weight, const uint16_t* scale, const u
 
 size_t cudalm_w4a16_packed_bytes(int N, int K) {
   if (N < 1 || K <= 0 || K % kGroup != 0) return 0;
-  return static_cast<size_t>((N + 15) / 16) * (K / kGroup) * kPackedBlock;
+  return static_cast<size_t>((N + 15) / 16) * packed_tile_bytes(K / kGroup);
 }
 
 int cudalm_w4a16_repack(const uint8_t* weight, const uint16_t* scale, void* packed, int N, int K,
@@ -747,10 +763,10 @@ int cudalm_w4a16_dequant_f32(const uint8_t* weight, const uint16_t* scale, int8_
 int cudalm_w4a16_kernel_regs(int variant) {
   switch (variant) {
     case CUDALM_W4A16_VARIANT_AUTO:
-    case CUDALM_W4A16_VARIANT_STREAM: return regs_of(w4a16_stream_kernel<true>);
+    case CUDALM_W4A16_VARIANT_STREAM: return regs_of(w4a16_stream_kernel<true, 1, false>);
     case CUDALM_W4A16_VARIANT_TILE16: return regs_of(w4a16_tile_kernel<1, 1, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_TILE32: return regs_of(w4a16_tile_kernel<1, 2, 4, 1, 8, true>);
-    case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_tile_kernel<4, 4, 2, 2, 2, true>);
+    case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_tile_kernel<2, 4, 2, 2, 2, true>);
     case CUDALM_W4A16_VARIANT_BYTEWISE: return regs_of(w4a16_bytewise_kernel);
     default: return -1;
   }

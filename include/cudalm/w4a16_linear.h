@@ -21,7 +21,7 @@ struct W4A16LinearView {
   int K = 0;
 };
 
-// Repacked layout: ceil(N/16) * (K/128) blocks of 1056 bytes.
+// Repacked layout: ceil(N/16) tiles of (K/128) * 1024 + 256 * ceil(K/1024) bytes.
 struct PackedW4A16Linear {
   void* packed = nullptr;  // device buffer owned by the caller
   int N = 0;

@@ -56,31 +56,34 @@ def test_shape_preconditions_rejected_before_device(w4):
 
 
 def test_packed_bytes(w4):
-    assert w4.packed_bytes(16, 128) == 1056
-    assert w4.packed_bytes(17, 128) == 2 * 1056
+    assert w4.packed_bytes(16, 128) == 1024 + 256
+    assert w4.packed_bytes(17, 128) == 2 * (1024 + 256)
     assert w4.packed_bytes(248320, 1024) == 15520 * 8 * 1056
+    assert w4.packed_bytes(16, 3584) == 28 * 1024 + 16 * 64
     assert w4.packed_bytes(0, 128) == 0
     assert w4.packed_bytes(16, 100) == 0
 
 
 def _numpy_repack(W, S, N, K):
     G = K // 128
+    SP = 16 * ((G + 7) // 8)
     nt = (N + 15) // 16
     Wp = np.zeros((nt * 16, K // 2), np.uint8)
     Wp[:N] = W
-    Sp = np.zeros((nt * 16, G), np.uint16)
-    Sp[:N] = S
-    out = np.zeros((nt, G, 1056), np.uint8)
+    Sp = np.zeros((nt * 16, SP // 2), np.uint16)
+    Sp[:N, :G] = S
+    tiles = []
     for rt in range(nt):
-        for g in range(G):
-            for lane in range(64):
-                i, a = lane & 15, lane >> 4
-                out[rt, g, 16 * lane:16 * lane + 16] = Wp[rt * 16 + i, g * 64 + a * 16:g * 64 + a * 16 + 16]
-            out[rt, g, 1024:] = np.ascontiguousarray(Sp[rt * 16:rt * 16 + 16, g]).view(np.uint8)
-    return out.ravel()
+        wpart = np.zeros((G, 64, 16), np.uint8)
+        for lane in range(64):
+            i, a = lane & 15, lane >> 4
+            rows = Wp[rt * 16 + i].reshape(G, 64)
+            wpart[:, lane, :] = rows[:, a * 16:a * 16 + 16]
+        tiles.append(np.concatenate([wpart.ravel(), Sp[rt * 16:rt * 16 + 16].view(np.uint8).ravel()]))
+    return np.concatenate(tiles)
 
 
-@pytest.mark.parametrize("N,K", [(1, 128), (16, 256), (37, 384), (64, 1024)])
+@pytest.mark.parametrize("N,K", [(1, 128), (16, 256), (37, 384), (64, 1024), (20, 3584), (5, 2304)])
 def test_repack_host_layout(w4, orc, N, K):
     W, S, _ = orc.fixture_gemv(N + K, N, K)
     got = w4.repack_host(W, S, N, K)
@@ -108,7 +111,7 @@ int main() {
     assert res.returncode == 0, res.stderr
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stderr
-    assert out.stdout.split() == ["1056", str(2 * 2 * 1056)]
+    assert out.stdout.split() == ["1280", str(2 * (2 * 1024 + 256))]
 
 
 def test_cpp_entry_aborts_on_precondition(tmp_path, w4):
