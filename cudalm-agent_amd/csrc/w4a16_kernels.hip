@@ -206,6 +206,25 @@ __device__ __forceinline__ void stream_load(StreamUnit& u, const uint8_t* __rest
   }
 }
 
+// One group of one 16-row weight tile for the stream kernel: the offset
+// chain was computed once per workgroup (corr), the weight chain seeds from
+// it, and the epilogue applies this lane's row scale.
+template <int NR>
+__device__ __forceinline__ void stream_group(f32x4_t& acc, const u32x4_t* xgroup, u32x4_t w,
+                                             const float* corr_g, float s, int a) {
+  u32x4_t xa[4];
+  load_group_x(xa, xgroup, a);
+  f32x4_t c;
+  if constexpr (NR == 1) {
+    c = f32x4_t{corr_g[4 * a], 0.0f, 0.0f, 0.0f};
+  } else {
+    c = *reinterpret_cast<const f32x4_t*>(corr_g + 4 * a);
+  }
+  const f32x4_t tp = group_product(w, xa, c);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) acc[r] = __builtin_fmaf(s, tp[r], acc[r]);
+}
+
 template <bool PACKED, int NR, bool SVEC>
 __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
     const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
@@ -213,6 +232,8 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
   extern __shared__ u32x4_t xs[];
   const int G = K >> 7;
   const int pitch = (K >> 3) + 1;
+  // LDS: activations [M][pitch] blocks, then the offset table corr[G][16]
+  float* corr = reinterpret_cast<float*>(xs + M * pitch);
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   const int i = lane & 15, a = lane >> 4;
@@ -227,9 +248,18 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
   stream_load<PACKED, SVEC>(cur, W, S, N, K, G, min(t, ntiles - 1), 0, lane);
   stage_activations(xs, pitch, X, K, 0, M, 0, K);
   __syncthreads();
+  // -1.5 * sum_k x per (group, row): the same for every weight tile, so the
+  // workgroup computes it once (waves split the groups)
+  const u32x4_t* xrow = xs + min(i, M - 1) * pitch;
+  for (int g = wave; g < G; g += kStreamWaves) {
+    u32x4_t xa[4];
+    load_group_x(xa, xrow + g * 16, a);
+    const f32x4_t c = group_offset(xa);
+    if (i == 0) *reinterpret_cast<f32x4_t*>(corr + g * 16 + 4 * a) = c;
+  }
+  __syncthreads();
   if (!active) return;
 
-  const u32x4_t* xrow = xs + min(i, M - 1) * pitch;
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
   int u = 0;
   while (true) {
@@ -245,16 +275,18 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
                               lane);
     const int g0 = u * kUnit;
     const int gn = min(kUnit, G - g0);
+    if (gn == kUnit) {
+      // full unit: straight-line, so independent group chains interleave
 #pragma unroll
-    for (int gg = 0; gg < kUnit; ++gg) {
-      if (gg < gn) {
-        u32x4_t xa[4];
-        load_group_x(xa, xrow + (g0 + gg) * 16, a);
-        const f32x4_t tp = group_product(cur.w[gg], xa, group_offset(xa));
-        const float s = unit_scale(cur.s, gg);
+      for (int gg = 0; gg < kUnit; ++gg)
+        stream_group<NR>(acc, xrow + (g0 + gg) * 16, cur.w[gg], corr + (g0 + gg) * 16,
+                         unit_scale(cur.s, gg), a);
+    } else {
 #pragma unroll
-        for (int r = 0; r < NR; ++r) acc[r] = __builtin_fmaf(s, tp[r], acc[r]);
-      }
+      for (int gg = 0; gg < kUnit; ++gg)
+        if (gg < gn)
+          stream_group<NR>(acc, xrow + (g0 + gg) * 16, cur.w[gg], corr + (g0 + gg) * 16,
+                           unit_scale(cur.s, gg), a);
     }
     if (u == U - 1) {
       const int n = t * kTileRows + i;
@@ -563,7 +595,9 @@ bool allow_lds(F kernel, size_t bytes) {
                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
 }
 
-size_t stream_lds_bytes(int K, int M) { return static_cast<size_t>(M) * (K / 8 + 1) * 16; }
+size_t stream_lds_bytes(int K, int M) {
+  return static_cast<size_t>(M) * (K / 8 + 1) * 16 + static_cast<size_t>(K / kGroup) * 64;
+}
 
 int stream_occupancy() {
   static int occ = 0;

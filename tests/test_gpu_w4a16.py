@@ -26,7 +26,7 @@ CENSUS = [(16, 1024), (512, 1024), (1024, 2048), (1024, 3584), (2048, 1024), (35
 EDGE = [(1, 128), (3, 128), (5, 256), (9, 1024), (15, 1024), (1023, 1024)]
 VARIANTS_FOR_M = {
     # variant name -> predicate on (M, K) for applicability
-    "stream": lambda M, K: M <= 16 and M * (K // 8 + 1) * 16 <= 65536,
+    "stream": lambda M, K: M <= 16 and M * (K // 8 + 1) * 16 + (K // 128) * 64 <= 65536,
     "tile16": lambda M, K: True,
     "tile32": lambda M, K: True,
     "prefill": lambda M, K: True,
