@@ -24,6 +24,7 @@ from disk. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -60,6 +61,25 @@ def census_calls():
         for name, N, K in (FULL_ATTN if kind == "full" else DELTANET) + MLP:
             calls.append((li, name, N, K))
     return calls
+
+
+def census_groups(fused: bool):
+    """Launch groups of one decode step in call order. Fused groups are the
+    projections that read the same activations (in_proj_qkv/z/b/a, gate/up,
+    q/k/v)."""
+    groups = []
+    for li, kind in enumerate(layer_kinds()):
+        if kind == "full":
+            plan = [FULL_ATTN[:3], FULL_ATTN[3:], MLP[:2], MLP[2:]]
+        else:
+            plan = [DELTANET[:4], DELTANET[4:], MLP[:2], MLP[2:]]
+        for grp in plan:
+            items = [(li, name, N, K) for name, N, K in grp]
+            if fused:
+                groups.append(items)
+            else:
+                groups.extend([[it] for it in items])
+    return groups
 
 
 def algo_bytes(N: int, K: int, M: int) -> int:
@@ -216,7 +236,7 @@ def main():
     del c0
 
     extra = {}
-    # ---------------- census: 186 calls + LM head per decode step ----------------
+    # ---------------- census: 186 projections + LM head per decode step ----------------
     if not args.no_census:
         calls = census_calls()
         cw = {}
@@ -226,30 +246,39 @@ def main():
         census = {}
         for Mc in (1, 8, 32):
             xs = {Kc: synth_act(torch, Mc, Kc, 0xAC70 + Kc + Mc, dev) for Kc in (1024, 2048, 3584)}
-            ys = {}
-            for _, name, Nc, Kc in calls:
-                ys.setdefault(Nc, torch.empty((Mc, Nc), dtype=torch.bfloat16, device=dev))
+            ys = {(li, name): torch.empty((Mc, Nc), dtype=torch.bfloat16, device=dev)
+                  for li, name, Nc, Kc in calls}
             xh = synth_act(torch, Mc, K, 0x11AF + Mc, dev)
             yh = torch.empty((Mc, N), dtype=torch.bfloat16, device=dev)
-            seq = [(cw[(li, name)].data_ptr(), xs[Kc].data_ptr(), ys[Nc].data_ptr(), Nc, Kc)
-                   for li, name, Nc, Kc in calls]
-            seq.append((packs[0].data_ptr(), xh.data_ptr(), yh.data_ptr(), N, K))
+            tot_bytes = sum(algo_bytes(Nc, Kc, Mc) for _, _, Nc, Kc in calls) + algo_bytes(N, K, Mc)
+            for fused in (False, True):
+                launches = []  # (list of (packed_ptr, y_ptr, N), K)
+                for group in census_groups(fused):
+                    Kc = group[0][3]
+                    launches.append(([(cw[(li, nm)].data_ptr(), ys[(li, nm)].data_ptr(), Nc)
+                                      for li, nm, Nc, _ in group], Kc))
+                launches.append(([(packs[0].data_ptr(), yh.data_ptr(), N)], K))
+                arrays = [(w4.proj_array([(pp, None, yy, nn) for pp, yy, nn in items]), len(items),
+                           xs[Kc].data_ptr() if (items[0][0] != packs[0].data_ptr()) else xh.data_ptr(), Kc)
+                          for items, Kc in launches]
 
-            def traversal(seq=seq, Mc=Mc):
-                for pp, xx, yy, Nc, Kc in seq:
-                    lib.cudalm_w4a16_gemv_bf16_prepacked(pp, xx, yy, Nc, Kc, Mc, sraw)
+                def traversal(arrays=arrays, Mc=Mc):
+                    for arr, cnt, xx, Kc in arrays:
+                        if cnt == 1:
+                            p0 = arr[0]
+                            lib.cudalm_w4a16_gemv_bf16_prepacked(p0.weight, xx, p0.y, p0.N, Kc, Mc, sraw)
+                        else:
+                            lib.cudalm_w4a16_gemv_bf16_multi(ctypes.cast(arr, ctypes.c_void_p), cnt, xx,
+                                                             Kc, Mc, 1, sraw)
 
-            t = graph_time(torch, traversal, 10, stream)
-            tot_bytes = sum(algo_bytes(Nc, Kc, Mc) for _, _, _, Nc, Kc in seq)
-            proj_bytes = sum(algo_bytes(Nc, Kc, Mc) for _, _, _, Nc, Kc in seq[:-1])
-            census[f"M{Mc}"] = {
-                "us_per_decode_step": round(t * 1e6, 2),
-                "calls": len(seq),
-                "bytes": tot_bytes,
-                "GBps": round(tot_bytes / t / 1e9, 1),
-                "frac_hbm_peak": round(tot_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
-                "projection_bytes_no_lm_head": proj_bytes,
-            }
+                t = graph_time(torch, traversal, 10, stream)
+                census[f"M{Mc}" + ("_fused" if fused else "")] = {
+                    "us_per_decode_step": round(t * 1e6, 2),
+                    "launches": len(arrays),
+                    "bytes": tot_bytes,
+                    "GBps": round(tot_bytes / t / 1e9, 1),
+                    "frac_hbm_peak": round(tot_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                }
         extra["census"] = census
         del cw
 

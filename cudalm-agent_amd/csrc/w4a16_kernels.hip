@@ -166,6 +166,28 @@ __device__ __forceinline__ void stage_activations(u32x4_t* xs, int pitch,
 // ---------------------------------------------------------------------------
 
 constexpr int kStreamWaves = 4;
+constexpr int kMaxProj = CUDALM_W4A16_MAX_PROJ;
+
+// Projections that share one activation matrix, streamed by one launch.
+// Tiles are numbered globally; projection j owns tiles
+// [tile_end[j-1], tile_end[j]).
+struct ProjTable {
+  const uint8_t* w[kMaxProj];
+  const uint16_t* s[kMaxProj];
+  uint16_t* y[kMaxProj];
+  int n[kMaxProj];
+  int tile_end[kMaxProj];
+  int count;
+};
+
+__device__ __forceinline__ int proj_of(const ProjTable& P, int t) {
+  int j = 0;
+  while (j < P.count - 1 && t >= P.tile_end[j]) ++j;
+  return j;
+}
+__device__ __forceinline__ int proj_begin(const ProjTable& P, int j) {
+  return j == 0 ? 0 : P.tile_end[j - 1];
+}
 
 struct StreamUnit {
   u32x4_t w[kUnit];
@@ -206,38 +228,60 @@ __device__ __forceinline__ void stream_load(StreamUnit& u, const uint8_t* __rest
   }
 }
 
-// One group of one 16-row weight tile for the stream kernel: the offset
-// chain was computed once per workgroup (corr), the weight chain seeds from
-// it, and the epilogue applies this lane's row scale.
-template <int NR>
-__device__ __forceinline__ void stream_group(f32x4_t& acc, const u32x4_t* xgroup, u32x4_t w,
-                                             const float* corr_g, float s, int a) {
-  u32x4_t xa[4];
-  load_group_x(xa, xgroup, a);
-  f32x4_t c;
-  if constexpr (NR == 1) {
-    c = f32x4_t{corr_g[4 * a], 0.0f, 0.0f, 0.0f};
-  } else {
-    c = *reinterpret_cast<const f32x4_t*>(corr_g + 4 * a);
-  }
-  const f32x4_t tp = group_product(w, xa, c);
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = __builtin_fmaf(s, tp[r], acc[r]);
+template <bool PACKED, bool SVEC>
+__device__ __forceinline__ void stream_load_t(StreamUnit& u, const ProjTable& P, int K, int G,
+                                              int t, int g0, int lane) {
+  const int j = proj_of(P, t);
+  stream_load<PACKED, SVEC>(u, P.w[j], P.s[j], P.n[j], K, G, t - proj_begin(P, j), g0, lane);
 }
 
-template <bool PACKED, int NR, bool SVEC>
+// One group of one 16-row weight tile against CT 16-row activation tiles:
+// the offset chain comes from the workgroup's table (corr_g), the weight
+// chain seeds from it, and the epilogue applies this lane's row scale.
+template <int NR, int CT>
+__device__ __forceinline__ void stream_group(f32x4_t (&acc)[CT], const u32x4_t* const (&xrow)[CT],
+                                             int g, u32x4_t w, const float* corr_g, float s,
+                                             int a) {
+  u32x4_t xa[CT][4];
+  f32x4_t t[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    load_group_x(xa[ct], xrow[ct] + g * 16, a);
+    if constexpr (NR == 1) {
+      t[ct] = f32x4_t{corr_g[ct * 16 + 4 * a], 0.0f, 0.0f, 0.0f};
+    } else {
+      t[ct] = *reinterpret_cast<const f32x4_t*>(corr_g + ct * 16 + 4 * a);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const u32x4_t B = decode_nibbles(w[d]);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) t[ct] = mfma16(xa[ct][d], B, t[ct]);
+  }
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[ct][r] = __builtin_fmaf(s, t[ct][r], acc[ct][r]);
+}
+
+// Stream kernel: M <= 16 * CT, all of x resident in LDS; waves stream
+// 16-row weight tiles of every projection in P (grid-stride) in units of
+// up to 8 groups, prefetching the next unit while the current one is
+// multiplied. NR = accumulator rows per lane that can hold outputs (1 when
+// M == 1, else 4).
+template <bool PACKED, int NR, bool SVEC, int CT>
 __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
-    const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
-    const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, int N, int K, int M) {
+    const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
   extern __shared__ u32x4_t xs[];
   const int G = K >> 7;
   const int pitch = (K >> 3) + 1;
-  // LDS: activations [M][pitch] blocks, then the offset table corr[G][16]
+  // LDS: activations [M][pitch] blocks, then the offset table corr[G][16*CT]
   float* corr = reinterpret_cast<float*>(xs + M * pitch);
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   const int i = lane & 15, a = lane >> 4;
-  const int ntiles = (N + kTileRows - 1) / kTileRows;
+  const int ntiles = P.tile_end[P.count - 1];
   const int U = (G + kUnit - 1) / kUnit;
   const int stride = gridDim.x * kStreamWaves;
   int t = blockIdx.x * kStreamWaves + wave;
@@ -245,22 +289,29 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
 
   // first unit's weights fly while the activations are staged
   StreamUnit cur, nxt;
-  stream_load<PACKED, SVEC>(cur, W, S, N, K, G, min(t, ntiles - 1), 0, lane);
+  stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t, ntiles - 1), 0, lane);
   stage_activations(xs, pitch, X, K, 0, M, 0, K);
   __syncthreads();
   // -1.5 * sum_k x per (group, row): the same for every weight tile, so the
   // workgroup computes it once (waves split the groups)
-  const u32x4_t* xrow = xs + min(i, M - 1) * pitch;
+  const u32x4_t* xrow[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) xrow[ct] = xs + min(ct * 16 + i, M - 1) * pitch;
   for (int g = wave; g < G; g += kStreamWaves) {
-    u32x4_t xa[4];
-    load_group_x(xa, xrow + g * 16, a);
-    const f32x4_t c = group_offset(xa);
-    if (i == 0) *reinterpret_cast<f32x4_t*>(corr + g * 16 + 4 * a) = c;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      u32x4_t xa[4];
+      load_group_x(xa, xrow[ct] + g * 16, a);
+      const f32x4_t c = group_offset(xa);
+      if (i == 0) *reinterpret_cast<f32x4_t*>(corr + (g * CT + ct) * 16 + 4 * a) = c;
+    }
   }
   __syncthreads();
   if (!active) return;
 
-  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t acc[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) acc[ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   int u = 0;
   while (true) {
     int nt = t, nu = u + 1;
@@ -271,32 +322,39 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
     const bool has_next = nt < ntiles;
     // past the last unit, re-read the current one (cache hits) instead of
     // branching around the loads
-    stream_load<PACKED, SVEC>(nxt, W, S, N, K, G, has_next ? nt : t, has_next ? nu * kUnit : u * kUnit,
-                              lane);
+    stream_load_t<PACKED, SVEC>(nxt, P, K, G, has_next ? nt : t, has_next ? nu * kUnit : u * kUnit,
+                                lane);
     const int g0 = u * kUnit;
     const int gn = min(kUnit, G - g0);
     if (gn == kUnit) {
       // full unit: straight-line, so independent group chains interleave
 #pragma unroll
       for (int gg = 0; gg < kUnit; ++gg)
-        stream_group<NR>(acc, xrow + (g0 + gg) * 16, cur.w[gg], corr + (g0 + gg) * 16,
-                         unit_scale(cur.s, gg), a);
+        stream_group<NR, CT>(acc, xrow, g0 + gg, cur.w[gg], corr + (g0 + gg) * 16 * CT,
+                             unit_scale(cur.s, gg), a);
     } else {
 #pragma unroll
       for (int gg = 0; gg < kUnit; ++gg)
         if (gg < gn)
-          stream_group<NR>(acc, xrow + (g0 + gg) * 16, cur.w[gg], corr + (g0 + gg) * 16,
-                           unit_scale(cur.s, gg), a);
+          stream_group<NR, CT>(acc, xrow, g0 + gg, cur.w[gg], corr + (g0 + gg) * 16 * CT,
+                               unit_scale(cur.s, gg), a);
     }
     if (u == U - 1) {
-      const int n = t * kTileRows + i;
+      const int j = proj_of(P, t);
+      const int Nj = P.n[j];
+      const int n = (t - proj_begin(P, j)) * kTileRows + i;
+      uint16_t* Yj = P.y[j];
 #pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const int m = 4 * a + r;
-        if (m < M && n < N)
-          Y[static_cast<size_t>(m) * N + n] = static_cast<uint16_t>(f32_to_bf16_rne(16.0f * acc[r]));
+      for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const int m = ct * 16 + 4 * a + r;
+          if (m < M && n < Nj)
+            Yj[static_cast<size_t>(m) * Nj + n] =
+                static_cast<uint16_t>(f32_to_bf16_rne(16.0f * acc[ct][r]));
+        }
+        acc[ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
       }
-      acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
     if (!has_next) break;
     cur = nxt;
@@ -544,7 +602,6 @@ __global__ __launch_bounds__(256) void w4a16_repack_kernel(
 // host launch layer
 // ---------------------------------------------------------------------------
 
-constexpr size_t kStreamLdsBudget = 64 * 1024;
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
@@ -595,14 +652,19 @@ bool allow_lds(F kernel, size_t bytes) {
                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
 }
 
+constexpr size_t kLdsMax = 160 * 1024;
+
 size_t stream_lds_bytes(int K, int M) {
-  return static_cast<size_t>(M) * (K / 8 + 1) * 16 + static_cast<size_t>(K / kGroup) * 64;
+  const int CT = M > 16 ? 2 : 1;
+  return static_cast<size_t>(M) * (K / 8 + 1) * 16 + static_cast<size_t>(K / kGroup) * 64 * CT;
 }
+
+bool stream_fits(int K, int M) { return M <= 32 && stream_lds_bytes(K, M) <= kLdsMax; }
 
 int stream_occupancy() {
   static int occ = 0;
   if (occ == 0) {
-    int v = 4;
+    int v = 3;
     if (const char* e = getenv("CUDALM_W4A16_STREAM_WGS_PER_CU")) {
       const int p = atoi(e);
       if (p >= 1 && p <= 32) v = p;
@@ -612,29 +674,49 @@ int stream_occupancy() {
   return occ;
 }
 
-template <bool PACKED, int NR, bool SVEC>
-int launch_stream_t(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
-                    int K, int M, hipStream_t stream) {
+template <bool PACKED, int NR, bool SVEC, int CT>
+int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   const size_t lds = stream_lds_bytes(K, M);
-  const int ntiles = (N + kTileRows - 1) / kTileRows;
+  const int ntiles = P.tile_end[P.count - 1];
   const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
-  const int cap = cu_count() * stream_occupancy();
+  int per_cu = stream_occupancy();
+  const int lds_fit = static_cast<int>(kLdsMax / (lds > 0 ? lds : 1));
+  if (lds_fit < per_cu) per_cu = lds_fit > 0 ? lds_fit : 1;
+  const int cap = cu_count() * per_cu;
   const int grid = want < cap ? want : cap;
-  hipLaunchKernelGGL((w4a16_stream_kernel<PACKED, NR, SVEC>), dim3(grid), dim3(kStreamWaves * 64),
-                     lds, stream, W, S, X, Y, N, K, M);
+  auto kern = w4a16_stream_kernel<PACKED, NR, SVEC, CT>;
+  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kStreamWaves * 64), lds, stream, P, X, K, M);
   return launch_status();
 }
 
 template <bool PACKED>
-int launch_stream(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
-                  int K, int M, hipStream_t stream) {
+int launch_stream(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   const int G = K / kGroup;
-  const bool svec = !PACKED && (G % 8 == 0) && aligned(S, 16);
+  bool svec = false;
+  if (!PACKED && G % 8 == 0) {
+    svec = true;
+    for (int j = 0; j < P.count; ++j) svec = svec && aligned(P.s[j], 16);
+  }
+  if (M > 16)
+    return svec ? launch_stream_t<PACKED, 4, true, 2>(P, X, K, M, stream)
+                : launch_stream_t<PACKED, 4, false, 2>(P, X, K, M, stream);
   if (M == 1)
-    return svec ? launch_stream_t<PACKED, 1, true>(W, S, X, Y, N, K, M, stream)
-                : launch_stream_t<PACKED, 1, false>(W, S, X, Y, N, K, M, stream);
-  return svec ? launch_stream_t<PACKED, 4, true>(W, S, X, Y, N, K, M, stream)
-              : launch_stream_t<PACKED, 4, false>(W, S, X, Y, N, K, M, stream);
+    return svec ? launch_stream_t<PACKED, 1, true, 1>(P, X, K, M, stream)
+                : launch_stream_t<PACKED, 1, false, 1>(P, X, K, M, stream);
+  return svec ? launch_stream_t<PACKED, 4, true, 1>(P, X, K, M, stream)
+              : launch_stream_t<PACKED, 4, false, 1>(P, X, K, M, stream);
+}
+
+ProjTable single_table(const uint8_t* W, const uint16_t* S, uint16_t* Y, int N) {
+  ProjTable P = {};
+  P.w[0] = W;
+  P.s[0] = S;
+  P.y[0] = Y;
+  P.n[0] = N;
+  P.tile_end[0] = (N + kTileRows - 1) / kTileRows;
+  P.count = 1;
+  return P;
 }
 
 template <int RB, int CT, int WN, int WM, int GPC, bool PACKED>
@@ -663,25 +745,33 @@ int launch_bytewise(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint
   return launch_status();
 }
 
-bool stream_fits(int K, int M) { return M <= 16 && stream_lds_bytes(K, M) <= kStreamLdsBudget; }
 
 template <bool PACKED>
 int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N, int K,
              int M, int variant, hipStream_t stream) {
   if (variant == CUDALM_W4A16_VARIANT_AUTO) {
-    if (stream_fits(K, M))
+    if (stream_fits(K, M)) {
       variant = CUDALM_W4A16_VARIANT_STREAM;
-    else if (M <= 16)
+    } else if (M <= 32 && M > 16) {
+      // x does not fit in LDS at once: 16-row column passes
+      for (int m0 = 0; m0 < M; m0 += 16) {
+        const int mc = M - m0 < 16 ? M - m0 : 16;
+        if (int rc = dispatch<PACKED>(W, S, X + static_cast<size_t>(m0) * K,
+                                      Y + static_cast<size_t>(m0) * N, N, K, mc,
+                                      CUDALM_W4A16_VARIANT_AUTO, stream))
+          return rc;
+      }
+      return CUDALM_W4A16_OK;
+    } else if (M <= 16) {
       variant = CUDALM_W4A16_VARIANT_TILE16;
-    else if (M <= 32)
-      variant = CUDALM_W4A16_VARIANT_TILE32;
-    else
+    } else {
       variant = CUDALM_W4A16_VARIANT_PREFILL;
+    }
   }
   switch (variant) {
     case CUDALM_W4A16_VARIANT_STREAM:
       if (!stream_fits(K, M)) return CUDALM_W4A16_EVARIANT;
-      return launch_stream<PACKED>(W, S, X, Y, N, K, M, stream);
+      return launch_stream<PACKED>(single_table(W, S, Y, N), X, K, M, stream);
     case CUDALM_W4A16_VARIANT_TILE16:
       return launch_tile<1, 1, 4, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
     case CUDALM_W4A16_VARIANT_TILE32:
@@ -707,7 +797,7 @@ int regs_of(F kernel) {
 
 extern "C" {
 
-int cudalm_w4a16_version(void) { return 200; }
+int cudalm_w4a16_version(void) { return 300; }
 
 const char* cudalm_w4a16_strerror(int code) {
   switch (code) {
@@ -780,6 +870,47 @@ int cudalm_w4a16_gemv_bf16_prepacked(const void* packed, const uint16_t* x, uint
                                                   CUDALM_W4A16_VARIANT_AUTO, stream);
 }
 
+int cudalm_w4a16_gemv_bf16_multi(const cudalm_w4a16_proj* projs, int count, const uint16_t* x,
+                                 int K, int M, int prepacked, hipStream_t stream) {
+  if (count < 1 || count > CUDALM_W4A16_MAX_PROJ) return CUDALM_W4A16_EINVAL;
+  if (!projs || !x) return CUDALM_W4A16_ENULL;
+  bool vec_ok = aligned(x, 16);
+  for (int j = 0; j < count; ++j) {
+    if (int rc = check_shape(projs[j].N, K, M)) return rc;
+    if (!projs[j].weight || !projs[j].y || (!prepacked && !projs[j].scale)) return CUDALM_W4A16_ENULL;
+    vec_ok = vec_ok && aligned(projs[j].weight, 16) && aligned(projs[j].y, 2) &&
+             (prepacked || aligned(projs[j].scale, 2));
+  }
+  if (prepacked && !vec_ok) return CUDALM_W4A16_EALIGN;
+  long long tiles = 0;
+  for (int j = 0; j < count; ++j) tiles += (projs[j].N + kTileRows - 1) / kTileRows;
+  if (!vec_ok || !stream_fits(K, M) || tiles > (1LL << 30)) {
+    // not one fused launch: one call per projection (same bits)
+    for (int j = 0; j < count; ++j) {
+      const int rc =
+          prepacked ? cudalm_w4a16_gemv_bf16_prepacked(projs[j].weight, x, projs[j].y, projs[j].N,
+                                                       K, M, stream)
+                    : cudalm_w4a16_gemv_bf16(static_cast<const uint8_t*>(projs[j].weight),
+                                             projs[j].scale, x, projs[j].y, projs[j].N, K, M,
+                                             stream);
+      if (rc) return rc;
+    }
+    return CUDALM_W4A16_OK;
+  }
+  ProjTable P = {};
+  int acc_tiles = 0;
+  for (int j = 0; j < count; ++j) {
+    P.w[j] = static_cast<const uint8_t*>(projs[j].weight);
+    P.s[j] = projs[j].scale;
+    P.y[j] = projs[j].y;
+    P.n[j] = projs[j].N;
+    acc_tiles += (projs[j].N + kTileRows - 1) / kTileRows;
+    P.tile_end[j] = acc_tiles;
+  }
+  P.count = count;
+  return prepacked ? launch_stream<true>(P, x, K, M, stream) : launch_stream<false>(P, x, K, M, stream);
+}
+
 int cudalm_w4a16_dequant_f32(const uint8_t* weight, const uint16_t* scale, int8_t* q_out,
                              float* w_out, int N, int K, hipStream_t stream) {
   if (int rc = check_shape(N, K, 1)) return rc;
@@ -797,7 +928,7 @@ int cudalm_w4a16_dequant_f32(const uint8_t* weight, const uint16_t* scale, int8_
 int cudalm_w4a16_kernel_regs(int variant) {
   switch (variant) {
     case CUDALM_W4A16_VARIANT_AUTO:
-    case CUDALM_W4A16_VARIANT_STREAM: return regs_of(w4a16_stream_kernel<true, 1, false>);
+    case CUDALM_W4A16_VARIANT_STREAM: return regs_of(w4a16_stream_kernel<true, 1, false, 1>);
     case CUDALM_W4A16_VARIANT_TILE16: return regs_of(w4a16_tile_kernel<1, 1, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_TILE32: return regs_of(w4a16_tile_kernel<1, 2, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_tile_kernel<2, 4, 2, 2, 2, true>);

@@ -44,6 +44,7 @@ _SIGS = {
     "cudalm_w4a16_gemv_bf16_prepacked": ([_P, _P, _P, _I, _I, _I, _P], _I),
     "cudalm_w4a16_gemv_bf16_prepacked_variant": ([_P, _P, _P, _I, _I, _I, _I, _P], _I),
     "cudalm_w4a16_dequant_f32": ([_P, _P, _P, _P, _I, _I, _P], _I),
+    "cudalm_w4a16_gemv_bf16_multi": ([_P, _I, _P, _I, _I, _I, _P], _I),
     "cudalm_w4a16_kernel_regs": ([_I], _I),
 }
 for _name, (_args, _ret) in _SIGS.items():
@@ -77,7 +78,13 @@ VARIANTS = {
 }
 
 GROUP = 128
-PACKED_BLOCK_BYTES = 1056
+MAX_PROJ = 8
+
+
+class Proj(ctypes.Structure):
+    """struct cudalm_w4a16_proj (include/cudalm_w4a16.h)."""
+    _fields_ = [("weight", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("N", ctypes.c_int)]
 
 
 class W4A16Error(RuntimeError):
@@ -226,3 +233,27 @@ def dequant(weight, scale, N: int, K: int, want_q: bool = True, want_w: bool = T
                                        _stream(stream))
     _check(rc, "cudalm_w4a16_dequant_f32")
     return q, w
+
+
+def proj_array(items):
+    """items: (weight_ptr, scale_ptr_or_None, y_ptr, N) -> ctypes array of Proj."""
+    arr = (Proj * len(items))()
+    for k, (w, sc, y, n) in enumerate(items):
+        arr[k].weight, arr[k].scale, arr[k].y, arr[k].N = w, sc, y, n
+    return arr
+
+
+def gemv_multi(weights, scales, x, Ns, K: int, M: int = 1, ys=None, prepacked: bool = False,
+               stream=None):
+    """Several projections sharing x in one launch; returns the list of y."""
+    import torch
+
+    if ys is None:
+        ys = [torch.empty((M, n), dtype=torch.bfloat16, device=x.device) for n in Ns]
+    items = [(_ptr(w), None if (prepacked or s is None) else _ptr(s), _ptr(y), n)
+             for w, s, y, n in zip(weights, scales if scales is not None else [None] * len(Ns), ys, Ns)]
+    arr = proj_array(items)
+    rc = _lib.cudalm_w4a16_gemv_bf16_multi(ctypes.cast(arr, ctypes.c_void_p), len(items), _ptr(x),
+                                           K, M, int(prepacked), _stream(stream))
+    _check(rc, "cudalm_w4a16_gemv_bf16_multi")
+    return ys

@@ -94,6 +94,24 @@ int cudalm_w4a16_gemv_bf16_prepacked(const void* packed, const uint16_t* x,
                                      uint16_t* y, int N, int K, int M,
                                      hipStream_t stream);
 
+/* Several projections that read the same activations x[M, K] (the
+ * q/k/v, in_proj_qkv/z/b/a and gate/up groups of a decoder layer,
+ * src/runtime/qwen35_deltanet.cpp:166-181,236-243 and
+ * src/runtime/qwen35_full_attention.cpp:211-240), computed by one launch
+ * when M <= 32 and x fits on chip, else one launch per projection. Each
+ * y_j is bit-identical to the single-projection call. No counterpart in the
+ * reference (it issues one launch per projection). */
+#define CUDALM_W4A16_MAX_PROJ 8
+typedef struct cudalm_w4a16_proj {
+  const void* weight;    /* file layout [N, K/2] or prepacked */
+  const uint16_t* scale; /* fp16 [N, K/128]; ignored when prepacked */
+  uint16_t* y;           /* bf16 [M, N] */
+  int N;
+} cudalm_w4a16_proj;
+int cudalm_w4a16_gemv_bf16_multi(const cudalm_w4a16_proj* projs, int count,
+                                 const uint16_t* x, int K, int M, int prepacked,
+                                 hipStream_t stream);
+
 /* Dequantize through the kernels' own nibble decoder: q_out[N, K] int8 and
  * w_out[N, K] = q * f32(scale) (either output may be NULL). The weight base
  * must be 4 B aligned. Equivalent to the reference's dequant_reference
@@ -108,7 +126,7 @@ int cudalm_w4a16_dequant_f32(const uint8_t* weight, const uint16_t* scale,
  * the default dispatch except CUDALM_W4A16_VARIANT_BYTEWISE, which sums in
  * the reference's order and is within tolerance. */
 #define CUDALM_W4A16_VARIANT_AUTO 0
-#define CUDALM_W4A16_VARIANT_STREAM 1   /* M <= 16, x resident in LDS */
+#define CUDALM_W4A16_VARIANT_STREAM 1   /* M <= 32, x resident in LDS */
 #define CUDALM_W4A16_VARIANT_TILE16 2   /* 16 columns per wave, K chunked */
 #define CUDALM_W4A16_VARIANT_TILE32 3   /* 32 columns per wave, K chunked */
 #define CUDALM_W4A16_VARIANT_PREFILL 4  /* 64x64 per wave, 128x128 per group */

@@ -26,7 +26,8 @@ CENSUS = [(16, 1024), (512, 1024), (1024, 2048), (1024, 3584), (2048, 1024), (35
 EDGE = [(1, 128), (3, 128), (5, 256), (9, 1024), (15, 1024), (1023, 1024)]
 VARIANTS_FOR_M = {
     # variant name -> predicate on (M, K) for applicability
-    "stream": lambda M, K: M <= 16 and M * (K // 8 + 1) * 16 + (K // 128) * 64 <= 65536,
+    "stream": lambda M, K: M <= 32 and (M * (K // 8 + 1) * 16
+                                        + (K // 128) * 64 * (2 if M > 16 else 1)) <= 160 * 1024,
     "tile16": lambda M, K: True,
     "tile32": lambda M, K: True,
     "prefill": lambda M, K: True,
@@ -241,3 +242,36 @@ def test_cpp_reference_names(w4, orc, dev):
     w4.batch_int4_gemv_bf16(w, s, x, yb, N, K, B)
     assert np.array_equal(down(yb).reshape(B, N)[0], down(y1).reshape(N))
     assert w4.int4_gemv_bf16_rowtile4_regs() > 0
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 16, 17, 32, 40])
+@pytest.mark.parametrize("packed", [False, True])
+def test_multi_projection_equals_single(w4, orc, dev, M, packed):
+    # one launch for projections sharing x (in_proj_qkv/z/b/a group shapes
+    # plus a ragged N) == one call per projection, bit for bit
+    K = 1024
+    Ns = [6144, 2048, 16, 16, 37]
+    x = torch.from_numpy(orc.synth_act(0x3317 + M, M, K).view(np.int16)).to(dev).view(torch.bfloat16)
+    ws, ss, refs = [], [], []
+    for j, N in enumerate(Ns):
+        W, S = orc.synth_w4a16(0x7000 + 31 * j, N, K)
+        w, s, _ = up(dev, W, S, np.zeros((1, K), np.uint16))
+        if packed:
+            w = w4.repack(w, s, N, K)
+        ws.append(w)
+        ss.append(s)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        if packed:
+            w4.gemv_prepacked(w, x, N, K, M, y=y)
+        else:
+            w4.gemv(w, s, x, N, K, M, y=y)
+        refs.append(down(y).reshape(M, N))
+    ys = w4.gemv_multi(ws, ss, x, Ns, K, M, prepacked=packed)
+    for j, N in enumerate(Ns):
+        assert np.array_equal(down(ys[j]).reshape(M, N), refs[j]), (j, N)
+
+
+def test_multi_projection_rejects_bad_count(w4, dev):
+    x = torch.zeros((1, 128), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        w4.gemv_multi([], [], x, [], 128, 1)
