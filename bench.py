@@ -63,6 +63,21 @@ def census_calls():
     return calls
 
 
+PROFILE_LM_HEAD = os.path.join(REPO, "profiles", "w4a16_stream_lm_head_M1.md")
+
+
+def measured_traffic():
+    """HBM bytes per LM-head launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (copy-calibrated), or None."""
+    try:
+        for line in open(PROFILE_LM_HEAD):
+            if line.startswith("traffic_bytes_per_launch = "):
+                return int(float(line.split("=")[1]))
+    except OSError:
+        return None
+    return None
+
+
 def census_groups(fused: bool):
     """Launch groups of one decode step in call order. Fused groups are the
     projections that read the same activations (in_proj_qkv/z/b/a, gate/up,
@@ -160,7 +175,13 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--lm-head-only", action="store_true",
+                    help="headline workload only (for counter collection)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (x5), to scale HBM counters")
     args = ap.parse_args()
+    if args.lm_head_only:
+        args.no_census = args.no_prefill = args.no_cpu = True
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the W4A16 projection path runs on a single "
@@ -170,6 +191,15 @@ def main():
 
     import numpy as np
     import torch
+
+    if args.copy_calibration:
+        src = torch.empty(args.copy_calibration << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": args.copy_calibration << 20, "calls": 5}))
+        return
 
     import cudalm_w4a16 as w4
 
@@ -216,24 +246,28 @@ def main():
     value = nbytes / step_s / 1e9
     kern_gbs = nbytes / per_launch / 1e9
 
-    file_per, _ = time_launches(torch, [mk_file(w, s) for w, s in zip(ws, ss)],
+    file_per = float("nan")
+    if not args.lm_head_only:
+        file_per, _ = time_launches(torch, [mk_file(w, s) for w, s in zip(ws, ss)],
                                 min(args.steps, 100), args.warmup, stream)
-    file_gbs = nbytes / file_per / 1e9
+    file_gbs = nbytes / file_per / 1e9 if file_per == file_per else None
 
     # M = 1, N = 3584, K = 1024 (rotate 64 copies = 120 MB; a
-    # single 1.9 MB matrix would be served from cache)
-    N0, K0 = 3584, 1024
-    c0 = []
-    for c in range(64):
-        w, s = synth_weights(torch, N0, K0, 0x3584 + c, dev)
-        c0.append(w4.repack(w, s, N0, K0))
-    x0 = synth_act(torch, 1, K0, 0x3585, dev)
-    y0 = torch.empty((1, N0), dtype=torch.bfloat16, device=dev)
-    x0p, y0p = x0.data_ptr(), y0.data_ptr()
-    c0_launch = [(lambda pp=p.data_ptr(): lib.cudalm_w4a16_gemv_bf16_prepacked(pp, x0p, y0p, N0, K0, 1, sraw))
-                 for p in c0]
-    cfg0_s = graph_time(torch, lambda: [f() for f in c0_launch], 20, stream) / len(c0_launch)
-    del c0
+    cfg0_s = None
+    if not args.lm_head_only:
+        # single 1.9 MB matrix would be served from cache)
+        N0, K0 = 3584, 1024
+        c0 = []
+        for c in range(64):
+            w, s = synth_weights(torch, N0, K0, 0x3584 + c, dev)
+            c0.append(w4.repack(w, s, N0, K0))
+        x0 = synth_act(torch, 1, K0, 0x3585, dev)
+        y0 = torch.empty((1, N0), dtype=torch.bfloat16, device=dev)
+        x0p, y0p = x0.data_ptr(), y0.data_ptr()
+        c0_launch = [(lambda pp=p.data_ptr(): lib.cudalm_w4a16_gemv_bf16_prepacked(pp, x0p, y0p, N0, K0, 1, sraw))
+                     for p in c0]
+        cfg0_s = graph_time(torch, lambda: [f() for f in c0_launch], 20, stream) / len(c0_launch)
+        del c0
 
     extra = {}
     # ---------------- census: 186 projections + LM head per decode step ----------------
@@ -340,13 +374,16 @@ def main():
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic(),
+                     "traffic_source": "profiles/w4a16_stream_lm_head_M1.md (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0, copy-calibrated)",
                      "kernel": "w4a16_stream_kernel<true>",
                      "kernel_us": round(per_launch * 1e6, 3),
                      "algorithmic_bytes_per_launch": nbytes},
-        "file_layout_entry": {"kernel_us": round(file_per * 1e6, 3), "GBps": round(file_gbs, 1)},
-        "config0_M1_3584x1024": {"us": round(cfg0_s * 1e6, 3),
-                                 "GBps": round(algo_bytes(N0, K0, 1) / cfg0_s / 1e9, 1)},
+        "file_layout_entry": ({"kernel_us": round(file_per * 1e6, 3), "GBps": round(file_gbs, 1)}
+                              if file_gbs else None),
+        "config0_M1_3584x1024": ({"us": round(cfg0_s * 1e6, 3),
+                                  "GBps": round(algo_bytes(3584, 1024, 1) / cfg0_s / 1e9, 1)}
+                                 if cfg0_s else None),
         "cpu_baseline": cpu,
     }
     out.update(extra)
