@@ -265,36 +265,63 @@ __device__ __forceinline__ void stream_group(f32x4_t (&acc)[CT], const u32x4_t* 
     for (int r = 0; r < NR; ++r) acc[ct][r] = __builtin_fmaf(s, t[ct][r], acc[ct][r]);
 }
 
-// Stream kernel: M <= 16 * CT, all of x resident in LDS; waves stream
-// 16-row weight tiles of every projection in P (grid-stride) in units of
-// up to 8 groups, prefetching the next unit while the current one is
-// multiplied. NR = accumulator rows per lane that can hold outputs (1 when
-// M == 1, else 4).
-template <bool PACKED, int NR, bool SVEC, int CT>
-__global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
-    const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
-  extern __shared__ u32x4_t xs[];
+// Canonical accumulation, shared by every kernel: within one unit of 8
+// groups, part = fma(s_g, tmp_g, part) from part = 0 in group order; the
+// unit partials are then summed in unit order from 0. The split kernel
+// computes unit partials on different waves and reduces them in that order,
+// so it produces the same bits as the kernels that walk units serially.
+
+// One unit (up to 8 groups) of one weight tile into `part`.
+template <int NR, int CT>
+__device__ __forceinline__ void stream_unit(f32x4_t (&part)[CT], const StreamUnit& cu,
+                                            const u32x4_t* const (&xrow)[CT], const float* corr,
+                                            int g0, int gn, int a) {
+  if (gn == kUnit) {
+    // full unit: straight-line, so independent group chains interleave
+#pragma unroll
+    for (int gg = 0; gg < kUnit; ++gg)
+      stream_group<NR, CT>(part, xrow, g0 + gg, cu.w[gg], corr + (g0 + gg) * 16 * CT,
+                           unit_scale(cu.s, gg), a);
+  } else {
+#pragma unroll
+    for (int gg = 0; gg < kUnit; ++gg)
+      if (gg < gn)
+        stream_group<NR, CT>(part, xrow, g0 + gg, cu.w[gg], corr + (g0 + gg) * 16 * CT,
+                             unit_scale(cu.s, gg), a);
+  }
+}
+
+template <int NR, int CT>
+__device__ __forceinline__ void store_tile(const ProjTable& P, int t, const f32x4_t (&total)[CT],
+                                           int M, int i, int a) {
+  const int j = proj_of(P, t);
+  const int Nj = P.n[j];
+  const int n = (t - proj_begin(P, j)) * kTileRows + i;
+  uint16_t* Yj = P.y[j];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int m = ct * 16 + 4 * a + r;
+      if (m < M && n < Nj)
+        Yj[static_cast<size_t>(m) * Nj + n] =
+            static_cast<uint16_t>(f32_to_bf16_rne(16.0f * total[ct][r]));
+    }
+}
+
+// Workgroup prologue of the stream and split kernels: x into LDS (pair
+// order), then the -1.5 * sum_k x table per (group, row), which is the same
+// for every weight tile (waves split the groups). Returns the LDS offset
+// table; xrow[ct] is this lane's activation row of column tile ct.
+template <int CT>
+__device__ __forceinline__ float* stream_prologue(u32x4_t* xs, const u32x4_t* (&xrow)[CT],
+                                                  const uint16_t* __restrict__ X, int K, int M,
+                                                  int wave, int i, int a) {
   const int G = K >> 7;
   const int pitch = (K >> 3) + 1;
-  // LDS: activations [M][pitch] blocks, then the offset table corr[G][16*CT]
   float* corr = reinterpret_cast<float*>(xs + M * pitch);
-  const int lane = threadIdx.x & 63;
-  const int wave = wave_id();
-  const int i = lane & 15, a = lane >> 4;
-  const int ntiles = P.tile_end[P.count - 1];
-  const int U = (G + kUnit - 1) / kUnit;
-  const int stride = gridDim.x * kStreamWaves;
-  int t = blockIdx.x * kStreamWaves + wave;
-  const bool active = t < ntiles;
-
-  // first unit's weights fly while the activations are staged
-  StreamUnit cur, nxt;
-  stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t, ntiles - 1), 0, lane);
   stage_activations(xs, pitch, X, K, 0, M, 0, K);
   __syncthreads();
-  // -1.5 * sum_k x per (group, row): the same for every weight tile, so the
-  // workgroup computes it once (waves split the groups)
-  const u32x4_t* xrow[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) xrow[ct] = xs + min(ct * 16 + i, M - 1) * pitch;
   for (int g = wave; g < G; g += kStreamWaves) {
@@ -307,11 +334,39 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
     }
   }
   __syncthreads();
+  return corr;
+}
+
+// Stream kernel: M <= 16 * CT, all of x resident in LDS; waves stream
+// 16-row weight tiles of every projection in P (grid-stride) in units of
+// up to 8 groups, prefetching the next unit while the current one is
+// multiplied. NR = accumulator rows per lane that can hold outputs (1 when
+// M == 1, else 4).
+template <bool PACKED, int NR, bool SVEC, int CT>
+__global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
+    const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
+  extern __shared__ u32x4_t xs[];
+  const int G = K >> 7;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int i = lane & 15, a = lane >> 4;
+  const int ntiles = P.tile_end[P.count - 1];
+  const int U = (G + kUnit - 1) / kUnit;
+  const int stride = gridDim.x * kStreamWaves;
+  int t = blockIdx.x * kStreamWaves + wave;
+  const bool active = t < ntiles;
+
+  // first unit's weights fly while the activations are staged
+  StreamUnit cur, nxt;
+  stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t, ntiles - 1), 0, lane);
+  const u32x4_t* xrow[CT];
+  const float* corr = stream_prologue<CT>(xs, xrow, X, K, M, wave, i, a);
   if (!active) return;
 
-  f32x4_t acc[CT];
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t part[CT], total[CT];
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) acc[ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int ct = 0; ct < CT; ++ct) part[ct] = total[ct] = zero;
   int u = 0;
   while (true) {
     int nt = t, nu = u + 1;
@@ -325,41 +380,78 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
     stream_load_t<PACKED, SVEC>(nxt, P, K, G, has_next ? nt : t, has_next ? nu * kUnit : u * kUnit,
                                 lane);
     const int g0 = u * kUnit;
-    const int gn = min(kUnit, G - g0);
-    if (gn == kUnit) {
-      // full unit: straight-line, so independent group chains interleave
+    stream_unit<NR, CT>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
 #pragma unroll
-      for (int gg = 0; gg < kUnit; ++gg)
-        stream_group<NR, CT>(acc, xrow, g0 + gg, cur.w[gg], corr + (g0 + gg) * 16 * CT,
-                             unit_scale(cur.s, gg), a);
-    } else {
-#pragma unroll
-      for (int gg = 0; gg < kUnit; ++gg)
-        if (gg < gn)
-          stream_group<NR, CT>(acc, xrow, g0 + gg, cur.w[gg], corr + (g0 + gg) * 16 * CT,
-                               unit_scale(cur.s, gg), a);
+    for (int ct = 0; ct < CT; ++ct) {
+      total[ct] = total[ct] + part[ct];
+      part[ct] = zero;
     }
     if (u == U - 1) {
-      const int j = proj_of(P, t);
-      const int Nj = P.n[j];
-      const int n = (t - proj_begin(P, j)) * kTileRows + i;
-      uint16_t* Yj = P.y[j];
+      store_tile<NR, CT>(P, t, total, M, i, a);
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          const int m = ct * 16 + 4 * a + r;
-          if (m < M && n < Nj)
-            Yj[static_cast<size_t>(m) * Nj + n] =
-                static_cast<uint16_t>(f32_to_bf16_rne(16.0f * acc[ct][r]));
-        }
-        acc[ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      }
+      for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
     }
     if (!has_next) break;
     cur = nxt;
     t = nt;
     u = nu;
+  }
+}
+
+// Split kernel: few weight tiles, several units per tile (K >= 2048). A
+// workgroup takes TPR = max(1, 4/U) tiles; its waves compute the unit
+// partials of those tiles side by side, park them in LDS, and the unit
+// partials of each tile are summed in unit order. Same bits as the stream
+// kernel; shorter latency when tiles alone cannot fill the machine.
+template <bool PACKED, int NR, bool SVEC, int CT>
+__global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
+    const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
+  extern __shared__ u32x4_t xs[];
+  const int G = K >> 7;
+  const int pitch = (K >> 3) + 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int i = lane & 15, a = lane >> 4;
+  const int ntiles = P.tile_end[P.count - 1];
+  const int U = (G + kUnit - 1) / kUnit;
+  const int TPR = U >= kStreamWaves ? 1 : kStreamWaves / U;
+  const int nslots = TPR * U;
+  const int t0 = blockIdx.x * TPR;
+  // slot partials after the offset table: [nslots][CT][64 lanes] f32x4
+  f32x4_t* slots = reinterpret_cast<f32x4_t*>(
+      reinterpret_cast<float*>(xs + M * pitch) + G * 16 * CT);
+
+  // this wave's first slot loads fly while the activations are staged
+  StreamUnit cur;
+  {
+    const int sl = min(wave, nslots - 1);
+    stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t0 + sl / U, ntiles - 1), (sl % U) * kUnit, lane);
+  }
+  const u32x4_t* xrow[CT];
+  const float* corr = stream_prologue<CT>(xs, xrow, X, K, M, wave, i, a);
+
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int sl = wave; sl < nslots; sl += kStreamWaves) {
+    if (sl != wave)
+      stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t0 + sl / U, ntiles - 1), (sl % U) * kUnit,
+                                  lane);
+    f32x4_t part[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
+    const int g0 = (sl % U) * kUnit;
+    stream_unit<NR, CT>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) slots[(sl * CT + ct) * 64 + lane] = part[ct];
+  }
+  __syncthreads();
+  if (wave < TPR && t0 + wave < ntiles) {
+    f32x4_t total[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      total[ct] = zero;
+      for (int u = 0; u < U; ++u) total[ct] = total[ct] + slots[((wave * U + u) * CT + ct) * 64 + lane];
+    }
+    store_tile<NR, CT>(P, t0 + wave, total, M, i, a);
   }
 }
 
@@ -398,11 +490,13 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) xr[ct] = min(wm * CT * 16 + ct * 16 + i, mrows - 1) * pitch;
 
-  f32x4_t acc[RB][CT];
+  static_assert(kUnit % GPC == 0, "chunks must not straddle an 8-group unit");
+  // acc: the current unit's partial; total: unit partials summed in order
+  f32x4_t acc[RB][CT], total[RB][CT];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) acc[rb][ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int ct = 0; ct < CT; ++ct) acc[rb][ct] = total[rb][ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int g0 = 0; g0 < G; g0 += GPC) {
     const int ng = min(GPC, G - g0);
@@ -463,6 +557,15 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
               acc[rb][ct][r] = __builtin_fmaf(s[gl][rb], tp[rb][ct][r], acc[rb][ct][r]);
       }
     }
+    if ((g0 + ng) % kUnit == 0 || g0 + ng == G) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          total[rb][ct] = total[rb][ct] + acc[rb][ct];
+          acc[rb][ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
   }
 
 #pragma unroll
@@ -477,7 +580,7 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
         const int ml = wm * CT * 16 + ct * 16 + 4 * a + r;
         if (ml < mrows)
           Y[static_cast<size_t>(m0 + ml) * N + n] =
-              static_cast<uint16_t>(f32_to_bf16_rne(16.0f * acc[rb][ct][r]));
+              static_cast<uint16_t>(f32_to_bf16_rne(16.0f * total[rb][ct][r]));
       }
   }
 }
@@ -661,6 +764,20 @@ size_t stream_lds_bytes(int K, int M) {
 
 bool stream_fits(int K, int M) { return M <= 32 && stream_lds_bytes(K, M) <= kLdsMax; }
 
+int split_tiles_per_round(int K) {
+  const int U = (K / kGroup + kUnit - 1) / kUnit;
+  return U >= kStreamWaves ? 1 : kStreamWaves / U;
+}
+
+size_t split_lds_bytes(int K, int M) {
+  const int CT = M > 16 ? 2 : 1;
+  const int U = (K / kGroup + kUnit - 1) / kUnit;
+  return stream_lds_bytes(K, M) +
+         static_cast<size_t>(split_tiles_per_round(K)) * U * CT * 64 * 16;
+}
+
+bool split_fits(int K, int M) { return M <= 32 && split_lds_bytes(K, M) <= kLdsMax; }
+
 int stream_occupancy() {
   static int occ = 0;
   if (occ == 0) {
@@ -690,22 +807,46 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   return launch_status();
 }
 
-template <bool PACKED>
-int launch_stream(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
+template <bool PACKED, int NR, bool SVEC, int CT>
+int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
+  const size_t lds = split_lds_bytes(K, M);
+  const int ntiles = P.tile_end[P.count - 1];
+  const int tpr = split_tiles_per_round(K);
+  const int grid = (ntiles + tpr - 1) / tpr;
+  auto kern = w4a16_split_kernel<PACKED, NR, SVEC, CT>;
+  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kStreamWaves * 64), lds, stream, P, X, K, M);
+  return launch_status();
+}
+
+// Unit-parallel (split) when the tiles alone leave most of the machine
+// idle and each tile has several units; otherwise tile-serial streaming.
+bool prefer_split(const ProjTable& P, int K, int M) {
+  const int U = (K / kGroup + kUnit - 1) / kUnit;
+  return U >= 2 && split_fits(K, M) && P.tile_end[P.count - 1] < 2 * cu_count();
+}
+
+template <bool PACKED, bool SPLIT>
+int launch_stream_any(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   const int G = K / kGroup;
   bool svec = false;
   if (!PACKED && G % 8 == 0) {
     svec = true;
     for (int j = 0; j < P.count; ++j) svec = svec && aligned(P.s[j], 16);
   }
-  if (M > 16)
-    return svec ? launch_stream_t<PACKED, 4, true, 2>(P, X, K, M, stream)
-                : launch_stream_t<PACKED, 4, false, 2>(P, X, K, M, stream);
-  if (M == 1)
-    return svec ? launch_stream_t<PACKED, 1, true, 1>(P, X, K, M, stream)
-                : launch_stream_t<PACKED, 1, false, 1>(P, X, K, M, stream);
-  return svec ? launch_stream_t<PACKED, 4, true, 1>(P, X, K, M, stream)
-              : launch_stream_t<PACKED, 4, false, 1>(P, X, K, M, stream);
+#define W4A16_LAUNCH(NR, SV, CT)                                          \
+  (SPLIT ? launch_split_t<PACKED, NR, SV, CT>(P, X, K, M, stream)         \
+         : launch_stream_t<PACKED, NR, SV, CT>(P, X, K, M, stream))
+  if (M > 16) return svec ? W4A16_LAUNCH(4, true, 2) : W4A16_LAUNCH(4, false, 2);
+  if (M == 1) return svec ? W4A16_LAUNCH(1, true, 1) : W4A16_LAUNCH(1, false, 1);
+  return svec ? W4A16_LAUNCH(4, true, 1) : W4A16_LAUNCH(4, false, 1);
+#undef W4A16_LAUNCH
+}
+
+template <bool PACKED>
+int launch_stream(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
+  return prefer_split(P, K, M) ? launch_stream_any<PACKED, true>(P, X, K, M, stream)
+                               : launch_stream_any<PACKED, false>(P, X, K, M, stream);
 }
 
 ProjTable single_table(const uint8_t* W, const uint16_t* S, uint16_t* Y, int N) {
@@ -751,7 +892,8 @@ int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y
              int M, int variant, hipStream_t stream) {
   if (variant == CUDALM_W4A16_VARIANT_AUTO) {
     if (stream_fits(K, M)) {
-      variant = CUDALM_W4A16_VARIANT_STREAM;
+      const ProjTable P = single_table(W, S, Y, N);
+      return launch_stream<PACKED>(P, X, K, M, stream);
     } else if (M <= 32 && M > 16) {
       // x does not fit in LDS at once: 16-row column passes
       for (int m0 = 0; m0 < M; m0 += 16) {
@@ -771,7 +913,10 @@ int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y
   switch (variant) {
     case CUDALM_W4A16_VARIANT_STREAM:
       if (!stream_fits(K, M)) return CUDALM_W4A16_EVARIANT;
-      return launch_stream<PACKED>(single_table(W, S, Y, N), X, K, M, stream);
+      return launch_stream_any<PACKED, false>(single_table(W, S, Y, N), X, K, M, stream);
+    case CUDALM_W4A16_VARIANT_SPLIT:
+      if (!split_fits(K, M)) return CUDALM_W4A16_EVARIANT;
+      return launch_stream_any<PACKED, true>(single_table(W, S, Y, N), X, K, M, stream);
     case CUDALM_W4A16_VARIANT_TILE16:
       return launch_tile<1, 1, 4, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
     case CUDALM_W4A16_VARIANT_TILE32:
@@ -933,6 +1078,7 @@ int cudalm_w4a16_kernel_regs(int variant) {
     case CUDALM_W4A16_VARIANT_TILE32: return regs_of(w4a16_tile_kernel<1, 2, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_tile_kernel<2, 4, 2, 2, 2, true>);
     case CUDALM_W4A16_VARIANT_BYTEWISE: return regs_of(w4a16_bytewise_kernel);
+    case CUDALM_W4A16_VARIANT_SPLIT: return regs_of(w4a16_split_kernel<true, 1, false, 1>);
     default: return -1;
   }
 }

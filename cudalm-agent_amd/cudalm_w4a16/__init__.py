@@ -68,7 +68,9 @@ VARIANT_TILE16 = 2
 VARIANT_TILE32 = 3
 VARIANT_PREFILL = 4
 VARIANT_BYTEWISE = 5
+VARIANT_SPLIT = 6
 VARIANTS = {
+    "split": VARIANT_SPLIT,
     "auto": VARIANT_AUTO,
     "stream": VARIANT_STREAM,
     "tile16": VARIANT_TILE16,

@@ -28,6 +28,9 @@ VARIANTS_FOR_M = {
     # variant name -> predicate on (M, K) for applicability
     "stream": lambda M, K: M <= 32 and (M * (K // 8 + 1) * 16
                                         + (K // 128) * 64 * (2 if M > 16 else 1)) <= 160 * 1024,
+    "split": lambda M, K: M <= 32 and (M * (K // 8 + 1) * 16 + (K // 128) * 64 * (2 if M > 16 else 1)
+                                       + max(1, 4 // -(-K // 1024)) * -(-K // 1024) * (2 if M > 16 else 1)
+                                       * 1024) <= 160 * 1024,
     "tile16": lambda M, K: True,
     "tile32": lambda M, K: True,
     "prefill": lambda M, K: True,
