@@ -30,6 +30,7 @@ HIPCC_FLAGS = [
     "-ffp-contract=off",
     "-fno-strict-aliasing",
     "-Wno-unused-command-line-argument",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 
