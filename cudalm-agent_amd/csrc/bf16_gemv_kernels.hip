@@ -1,0 +1,279 @@
+// bf16 GEMV (the tied LM head) for MI355X (gfx950): kernels and the C-ABI
+// launch layer declared in include/cudalm_bf16_gemv.h.
+//
+// Contract (reference: include/cudalm/kernels/bf16_gemv.h:19-38,
+// src/kernels/bf16_gemv.cu:40-129, src/kernels/batch_decode.cu:195-236):
+//   y[m,n] = bf16_rne( sum_k f32(W[n,k]) * f32(x[m,k]) ), fp32 accumulation,
+//   W bf16 [N, K], x bf16 [M, K], y bf16 [M, N], all row-major.
+//
+// The weight is read exactly once per launch (for M <= 32 activation rows;
+// larger M is split into row chunks that each stream it). bf16 x bf16
+// products are exact in fp32, so the matrix cores compute the contraction
+// directly: v_mfma_f32_16x16x32_bf16 with activations as the A operand and
+// a 16-row weight tile as the B operand. Lane l = 16a + i of MFMA step j in
+// unit u holds 16 contiguous bytes of weight row i: k = 256u + 32j + 8a ..
+// +7, and reads the same k of its activation row from LDS. Every output is
+// one MFMA chain over k in ascending 32-wide steps, so its bits do not
+// depend on M, the chunking of M, or which wave or workgroup computed it.
+//
+// Workload of the LM head (N = 248320, K = 1024, M = 1): 508.6 MB of
+// weights, streamed by persistent waves that walk 16-row tiles grid-stride
+// in 8 KB units (256 k x 16 rows) and prefetch the next unit while the
+// current one is multiplied.
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+#include "cudalm_bf16_gemv.h"
+#include "hip_common.h"
+
+namespace {
+
+using namespace cudalm_hip;
+
+constexpr int kWaves = 4;              // waves per workgroup
+constexpr int kSteps = 8;              // MFMA steps per streamed unit
+constexpr int kUnitK = 32 * kSteps;    // k per unit
+constexpr int kTile = 16;              // weight rows per tile
+
+struct Bf16Unit {
+  u32x4_t w[kSteps];
+};
+
+// Straight-line loads (k clamped into the row); the k >= K lanes are zeroed
+// at use, so a partial last unit needs no branch around the loads.
+__device__ __forceinline__ void bf16_unit_load(Bf16Unit& v, const uint16_t* __restrict__ W, int N,
+                                               int K, int tile, int u, int lane) {
+  const int i = lane & 15, a = lane >> 4;
+  const uint16_t* wrow = W + static_cast<size_t>(min(tile * kTile + i, N - 1)) * K;
+#pragma unroll
+  for (int j = 0; j < kSteps; ++j)
+    v.w[j] = *reinterpret_cast<const u32x4_t*>(wrow + min(u * kUnitK + 32 * j + 8 * a, K - 8));
+}
+
+template <int CT>
+__device__ __forceinline__ void bf16_unit_mma(f32x4_t (&acc)[CT], const Bf16Unit& v,
+                                              const u32x4_t* const (&xrow)[CT], int u, int K,
+                                              int a) {
+  const u32x4_t zero4 = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < kSteps; ++j) {
+    const int kb = u * kUnitK + 32 * j;  // first k of the step
+    const u32x4_t b = kb + 8 * a < K ? v.w[j] : zero4;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) acc[ct] = mfma16(xrow[ct][(kb >> 3) + a], b, acc[ct]);
+  }
+}
+
+// Persistent stream kernel. Launch: grid (gx, ceil(M / mc)), 256 threads,
+// LDS = mc * (32 * ceil(K/256) + 1) * 16 bytes; chunk y covers activation
+// rows [y * mc, y * mc + mc) and mc <= 16 * CT. Requires K % 8 == 0 and
+// 16 B aligned W and X bases.
+template <int CT>
+__global__ __launch_bounds__(kWaves * 64) void bf16_gemv_stream_kernel(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
+    int N, int K, int M, int mc) {
+  extern __shared__ u32x4_t xs[];
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int i = lane & 15, a = lane >> 4;
+  const int U = (K + kUnitK - 1) / kUnitK;
+  const int pitch = U * (kUnitK / 8) + 1;  // 16 B blocks per LDS row (padded)
+  const int ntiles = (N + kTile - 1) / kTile;
+  const int m0 = blockIdx.y * mc;
+  const int mrows = min(mc, M - m0);
+  const int stride = gridDim.x * kWaves;
+  int t = blockIdx.x * kWaves + wave;
+
+  // first unit's weights fly while the activations are staged
+  Bf16Unit cur, nxt;
+  bf16_unit_load(cur, W, N, K, min(t, ntiles - 1), 0, lane);
+  const int nb = U * (kUnitK / 8);
+  for (int e = threadIdx.x; e < mrows * nb; e += blockDim.x) {
+    const int mm = e / nb;
+    const int b = e - mm * nb;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (8 * b < K)
+      v = *reinterpret_cast<const u32x4_t*>(X + static_cast<size_t>(m0 + mm) * K + 8 * b);
+    xs[mm * pitch + b] = v;
+  }
+  __syncthreads();
+  if (t >= ntiles) return;
+
+  const u32x4_t* xrow[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) xrow[ct] = xs + min(ct * 16 + i, mrows - 1) * pitch;
+
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t acc[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) acc[ct] = zero;
+  int u = 0;
+  while (true) {
+    int nt = t, nu = u + 1;
+    if (nu == U) {
+      nu = 0;
+      nt = t + stride;
+    }
+    const bool has_next = nt < ntiles;
+    // past the last unit, re-read the current one (cache hits) instead of
+    // branching around the loads
+    bf16_unit_load(nxt, W, N, K, has_next ? nt : t, has_next ? nu : u, lane);
+    bf16_unit_mma<CT>(acc, cur, xrow, u, K, a);
+    if (u == U - 1) {
+      const int n = t * kTile + i;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = ct * 16 + 4 * a + r;
+          if (m < mrows && n < N)
+            Y[static_cast<size_t>(m0 + m) * N + n] =
+                static_cast<uint16_t>(f32_to_bf16_rne(acc[ct][r]));
+        }
+        acc[ct] = zero;
+      }
+    }
+    if (!has_next) break;
+    cur = nxt;
+    t = nt;
+    u = nu;
+  }
+}
+
+// Element-wise fallback for K % 8 != 0, misaligned bases or rows too long
+// for LDS (the reference's scalar kernel, bf16_gemv.cu:78-110, serves the
+// same cases). One wave per (row n, activation row m): lane-strided fp32
+// partial sums, then a butterfly reduction over the wave.
+__global__ __launch_bounds__(kWaves * 64) void bf16_gemv_scalar_kernel(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
+    int N, int K) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * kWaves + wave_id();
+  const int m = blockIdx.y;
+  if (n >= N) return;
+  const uint16_t* wrow = W + static_cast<size_t>(n) * K;
+  const uint16_t* xrow = X + static_cast<size_t>(m) * K;
+  float acc = 0.0f;
+  for (int k = lane; k < K; k += 64) {
+    const float p = bf16_lo(wrow[k]) * bf16_lo(xrow[k]);
+    acc = acc + p;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
+  if (lane == 0) Y[static_cast<size_t>(m) * N + n] = static_cast<uint16_t>(f32_to_bf16_rne(acc));
+}
+
+size_t stream_lds(int K, int mc) {
+  const int U = (K + kUnitK - 1) / kUnitK;
+  return static_cast<size_t>(mc) * (U * (kUnitK / 8) + 1) * 16;
+}
+
+// Activation rows per chunk: up to 32 (two 16-row MFMA column tiles) when
+// M > 16, as many as the LDS holds; 0 if not even one row fits.
+int stream_rows_per_chunk(int K, int M) {
+  int mc = M > 16 ? 32 : M;
+  while (mc > 0 && stream_lds(K, mc) > kLdsMax) --mc;
+  return mc;
+}
+
+int stream_wgs_per_cu() {
+  static int occ = 0;
+  if (occ == 0) {
+    int v = 4;
+    if (const char* e = getenv("CUDALM_BF16_GEMV_WGS_PER_CU")) {
+      const int p = atoi(e);
+      if (p >= 1 && p <= 32) v = p;
+    }
+    occ = v;
+  }
+  return occ;
+}
+
+template <int CT>
+int launch_stream_ct(const uint16_t* W, const uint16_t* X, uint16_t* Y, int N, int K, int M,
+                     int mc, hipStream_t stream) {
+  const size_t lds = stream_lds(K, mc);
+  auto kern = bf16_gemv_stream_kernel<CT>;
+  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+  const int ntiles = (N + kTile - 1) / kTile;
+  const int per_cu = static_cast<int>(kLdsMax / lds) < stream_wgs_per_cu()
+                         ? static_cast<int>(kLdsMax / lds)
+                         : stream_wgs_per_cu();
+  const int need = (ntiles + kWaves - 1) / kWaves;
+  const int cap = cu_count() * (per_cu > 0 ? per_cu : 1);
+  const int gx = need < cap ? need : cap;
+  const int gy = (M + mc - 1) / mc;
+  if (gy > 65535) return CUDALM_W4A16_ERANGE;
+  hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(kWaves * 64), lds, stream, W, X, Y, N, K, M, mc);
+  return launch_status();
+}
+
+int launch_stream(const uint16_t* W, const uint16_t* X, uint16_t* Y, int N, int K, int M,
+                  hipStream_t stream) {
+  const int mc = stream_rows_per_chunk(K, M);
+  if (mc < 1) return CUDALM_W4A16_EVARIANT;
+  if (mc > 16) return launch_stream_ct<2>(W, X, Y, N, K, M, mc, stream);
+  return launch_stream_ct<1>(W, X, Y, N, K, M, mc, stream);
+}
+
+int launch_scalar(const uint16_t* W, const uint16_t* X, uint16_t* Y, int N, int K, int M,
+                  hipStream_t stream) {
+  if (M > 65535) return CUDALM_W4A16_ERANGE;
+  hipLaunchKernelGGL(bf16_gemv_scalar_kernel, dim3((N + kWaves - 1) / kWaves, M),
+                     dim3(kWaves * 64), 0, stream, W, X, Y, N, K);
+  return launch_status();
+}
+
+int check_shape(int N, int K, int M) {
+  if (N < 1 || M < 1 || K < 1) return CUDALM_W4A16_EINVAL;
+  if (static_cast<long long>(N) + kTile > (1LL << 30) || K > (1 << 28) ||
+      static_cast<long long>(M) > 65535LL * 32)
+    return CUDALM_W4A16_ERANGE;
+  return CUDALM_W4A16_OK;
+}
+
+bool stream_ok(const uint16_t* W, const uint16_t* X, int K, int M) {
+  return K % 8 == 0 && aligned(W, 16) && aligned(X, 16) && stream_rows_per_chunk(K, M) >= 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cudalm_bf16_gemv_variant(const uint16_t* weight, const uint16_t* x, uint16_t* y, int N, int K,
+                             int M, int variant, hipStream_t stream) {
+  if (int rc = check_shape(N, K, M)) return rc;
+  if (!weight || !x || !y) return CUDALM_W4A16_ENULL;
+  if (!aligned(weight, 2) || !aligned(x, 2) || !aligned(y, 2)) return CUDALM_W4A16_EALIGN;
+  const bool vec = stream_ok(weight, x, K, M);
+  switch (variant) {
+    case CUDALM_BF16_VARIANT_AUTO:
+      return vec ? launch_stream(weight, x, y, N, K, M, stream)
+                 : launch_scalar(weight, x, y, N, K, M, stream);
+    case CUDALM_BF16_VARIANT_STREAM:
+      if (!vec) return CUDALM_W4A16_EVARIANT;
+      return launch_stream(weight, x, y, N, K, M, stream);
+    case CUDALM_BF16_VARIANT_SCALAR:
+      return launch_scalar(weight, x, y, N, K, M, stream);
+    default:
+      return CUDALM_W4A16_EVARIANT;
+  }
+}
+
+int cudalm_bf16_gemv(const uint16_t* weight, const uint16_t* x, uint16_t* y, int N, int K, int M,
+                     hipStream_t stream) {
+  return cudalm_bf16_gemv_variant(weight, x, y, N, K, M, CUDALM_BF16_VARIANT_AUTO, stream);
+}
+
+int cudalm_bf16_gemv_kernel_regs(int variant) {
+  switch (variant) {
+    case CUDALM_BF16_VARIANT_STREAM: return regs_of(bf16_gemv_stream_kernel<1>);
+    case CUDALM_BF16_VARIANT_SCALAR: return regs_of(bf16_gemv_scalar_kernel);
+    default: return -1;
+  }
+}
+
+}  // extern "C"

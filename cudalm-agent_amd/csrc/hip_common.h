@@ -1,0 +1,96 @@
+// Device and launch helpers shared by the engine's kernel files (gfx950).
+#ifndef CUDALM_HIP_COMMON_H
+#define CUDALM_HIP_COMMON_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "cudalm_w4a16.h"
+
+namespace cudalm_hip {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr size_t kLdsMax = 160 * 1024;  // LDS per CU (and per workgroup) on gfx950
+
+// Wave index inside the workgroup, as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) {
+  return __builtin_bit_cast(float, v & 0xFFFF0000u);
+}
+
+// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  const uint32_t x = __builtin_bit_cast(uint32_t, f);
+  if ((x & 0x7F800000u) == 0x7F800000u && (x & 0x7FFFFFu)) return (x >> 16) | 0x40u;
+  return (x + 0x7FFFu + ((x >> 16) & 1u)) >> 16;
+}
+
+// D = A (16 rows x 32 k) * B (32 k x 16 cols) + C, bf16 in, fp32 accumulate.
+// Lane l = 16a + i: A row i / B column i, k = 8a .. 8a+7; D rows 4a..4a+3 of column i.
+__device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+inline bool aligned(const void* p, uintptr_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+// Compute units of the current device (cached per device).
+inline int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+inline int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? CUDALM_W4A16_OK : CUDALM_W4A16_ELAUNCH;
+}
+
+// Dynamic LDS above 64 KB must be opted into once per kernel.
+template <typename F>
+bool allow_lds(F kernel, size_t bytes) {
+  if (bytes <= 64 * 1024) return true;
+  static thread_local const void* done[64] = {nullptr};
+  for (auto& d : done) {
+    if (d == reinterpret_cast<const void*>(kernel)) return true;
+    if (d == nullptr) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(bytes > kLdsMax ? bytes : kLdsMax)) != hipSuccess)
+        return false;
+      d = reinterpret_cast<const void*>(kernel);
+      return true;
+    }
+  }
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             static_cast<int>(kLdsMax)) == hipSuccess;
+}
+
+template <typename F>
+int regs_of(F kernel) {
+  hipFuncAttributes attr;
+  if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel)) != hipSuccess) return -1;
+  return attr.numRegs;
+}
+
+}  // namespace cudalm_hip
+
+#endif

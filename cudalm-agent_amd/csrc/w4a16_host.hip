@@ -4,6 +4,8 @@
 // Reference interfaces replaced here:
 //   cudalm::int4_gemv_bf16                include/cudalm/kernels/int4_gemv_bf16.h:46-52
 //   cudalm::kernels::batch_int4_gemv_bf16 include/cudalm/kernels/batch_decode.h:61-67
+//   cudalm::bf16_gemv                     include/cudalm/kernels/bf16_gemv.h:37-38
+//   cudalm::kernels::batch_bf16_gemv      include/cudalm/kernels/batch_decode.h:77-79
 //   CUDALM_PRECONDITION / CUDA_CHECK_LAUNCH (abort)  include/cudalm/cuda_check.h:38-63
 
 #include <cstdio>
@@ -11,8 +13,10 @@
 #include <cstring>
 
 #include "cudalm/kernels/batch_decode.h"
+#include "cudalm/kernels/bf16_gemv.h"
 #include "cudalm/kernels/int4_gemv_bf16.h"
 #include "cudalm/w4a16_linear.h"
+#include "cudalm_bf16_gemv.h"
 #include "cudalm_w4a16.h"
 
 namespace cudalm {
@@ -41,6 +45,11 @@ std::uint16_t* bits(__hip_bfloat16* p) { return reinterpret_cast<std::uint16_t*>
 
 }  // namespace
 
+void bf16_gemv(const __hip_bfloat16* weight, const __hip_bfloat16* x, __hip_bfloat16* y, int N,
+               int K, hipStream_t stream) {
+  W4A16_CHECK("bf16_gemv", cudalm_bf16_gemv(bits(weight), bits(x), bits(y), N, K, 1, stream));
+}
+
 void int4_gemv_bf16(const std::uint8_t* weight, const __half* scales, const __hip_bfloat16* x,
                     __hip_bfloat16* y, int N, int K, hipStream_t stream) {
   W4A16_CHECK("int4_gemv_bf16",
@@ -50,6 +59,12 @@ void int4_gemv_bf16(const std::uint8_t* weight, const __half* scales, const __hi
 int int4_gemv_bf16_rowtile4_regs() { return cudalm_w4a16_kernel_regs(CUDALM_W4A16_VARIANT_STREAM); }
 
 namespace kernels {
+
+void batch_bf16_gemv(const __hip_bfloat16* weight, const __hip_bfloat16* x, __hip_bfloat16* y,
+                     int N, int K, int B, hipStream_t stream) {
+  W4A16_CHECK("batch_bf16_gemv",
+              cudalm_bf16_gemv(bits(weight), bits(x), bits(y), N, K, B, stream));
+}
 
 void batch_int4_gemv_bf16(const std::uint8_t* weight, const __half* scale,
                           const __hip_bfloat16* x, __hip_bfloat16* y, int N, int K, int B,

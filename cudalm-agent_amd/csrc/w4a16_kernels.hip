@@ -48,12 +48,12 @@
 #include <stdlib.h>
 
 #include "cudalm_w4a16.h"
+#include "hip_common.h"
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+using namespace cudalm_hip;
+
 
 constexpr int kGroup = 128;     // quantization group (k)
 constexpr int kTileRows = 16;   // weight rows per MFMA tile
@@ -69,21 +69,8 @@ __host__ __device__ constexpr size_t packed_tile_bytes(int G) {
 // device helpers
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ int wave_id() {
-  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-}
-
 __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
-}
-
-__device__ __forceinline__ float bf16_lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }
-
-// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
-__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
-  const uint32_t x = __builtin_bit_cast(uint32_t, f);
-  if ((x & 0x7F800000u) == 0x7F800000u && (x & 0x7FFFFFu)) return (x >> 16) | 0x40u;
-  return (x + 0x7FFFu + ((x >> 16) & 1u)) >> 16;
 }
 
 // 8 nibbles (k = 0..7 of a block, nibble k at bits 4k) -> 4 bf16 pairs
@@ -107,11 +94,6 @@ __device__ __forceinline__ u32x4_t pair_order(u32x4_t v) {
   p[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
   p[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
   return p;
-}
-
-__device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
 // -1.5 * (sum over the group of this lane-set's activation rows), as a 16x16
@@ -889,7 +871,6 @@ __global__ __launch_bounds__(256) void w4a16_repack_kernel(
 // ---------------------------------------------------------------------------
 
 
-bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 int check_shape(int N, int K, int M) {
   if (N < 1 || M < 1 || K <= 0 || K % kGroup != 0) return CUDALM_W4A16_EINVAL;
@@ -900,45 +881,6 @@ int check_shape(int N, int K, int M) {
   return CUDALM_W4A16_OK;
 }
 
-int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
-int launch_status() {
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? CUDALM_W4A16_OK : CUDALM_W4A16_ELAUNCH;
-}
-
-// Dynamic LDS above 64 KB must be opted into once per kernel.
-template <typename F>
-bool allow_lds(F kernel, size_t bytes) {
-  if (bytes <= 64 * 1024) return true;
-  static thread_local const void* done[64] = {nullptr};
-  for (auto& d : done) {
-    if (d == reinterpret_cast<const void*>(kernel)) return true;
-    if (d == nullptr) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(bytes > 160 * 1024 ? bytes : 160 * 1024)) != hipSuccess)
-        return false;
-      d = reinterpret_cast<const void*>(kernel);
-      return true;
-    }
-  }
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
-}
-
-constexpr size_t kLdsMax = 160 * 1024;
 
 size_t stream_lds_bytes(int K, int M) {
   const int CT = M > 16 ? 2 : 1;
@@ -1159,13 +1101,6 @@ int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y
   }
 }
 
-template <typename F>
-int regs_of(F kernel) {
-  hipFuncAttributes attr;
-  if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel)) != hipSuccess) return -1;
-  return attr.numRegs;
-}
-
 }  // namespace
 
 extern "C" {
@@ -1175,9 +1110,11 @@ int cudalm_w4a16_version(void) { return 300; }
 const char* cudalm_w4a16_strerror(int code) {
   switch (code) {
     case CUDALM_W4A16_OK: return "ok";
-    case CUDALM_W4A16_EINVAL: return "invalid shape: requires N >= 1, M >= 1, K > 0, K % 128 == 0";
+    case CUDALM_W4A16_EINVAL:
+      return "invalid shape: requires N >= 1, M >= 1, K > 0 (W4A16 entry points: K % 128 == 0)";
     case CUDALM_W4A16_ENULL: return "null pointer argument";
-    case CUDALM_W4A16_EALIGN: return "prepacked weight or activation base not 16-byte aligned";
+    case CUDALM_W4A16_EALIGN:
+      return "base misaligned (prepacked W4A16 buffers: 16 bytes; bf16 buffers: 2 bytes)";
     case CUDALM_W4A16_ELAUNCH: return "HIP kernel launch failed";
     case CUDALM_W4A16_ERANGE: return "shape exceeds the kernels' index range";
     case CUDALM_W4A16_EVARIANT: return "unknown or inapplicable kernel variant";

@@ -6,6 +6,8 @@ and benchmarks:
   int4_gemv_bf16(weight, scales, x, y, N, K)              int4_gemv_bf16.h:46-48
   batch_int4_gemv_bf16(weight, scale, x, y, N, K, B)      batch_decode.h:61-63
   int4_gemv_bf16_rowtile4_regs()                          int4_gemv_bf16.h:52
+  bf16_gemv(weight, x, y, N, K)                           bf16_gemv.h:37-38
+  batch_bf16_gemv(weight, x, y, N, K, B)                  batch_decode.h:77-79
 
 plus the load-time repack and the prepacked path. Arguments are torch
 tensors on the GPU (torch provides device memory and the stream; all
@@ -46,6 +48,9 @@ _SIGS = {
     "cudalm_w4a16_dequant_f32": ([_P, _P, _P, _P, _I, _I, _P], _I),
     "cudalm_w4a16_gemv_bf16_multi": ([_P, _I, _P, _I, _I, _I, _P], _I),
     "cudalm_w4a16_kernel_regs": ([_I], _I),
+    "cudalm_bf16_gemv": ([_P, _P, _P, _I, _I, _I, _P], _I),
+    "cudalm_bf16_gemv_variant": ([_P, _P, _P, _I, _I, _I, _I, _P], _I),
+    "cudalm_bf16_gemv_kernel_regs": ([_I], _I),
 }
 for _name, (_args, _ret) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -78,6 +83,12 @@ VARIANTS = {
     "prefill": VARIANT_PREFILL,
     "bytewise": VARIANT_BYTEWISE,
 }
+
+BF16_VARIANT_AUTO = 0
+BF16_VARIANT_STREAM = 1
+BF16_VARIANT_SCALAR = 2
+BF16_VARIANTS = {"auto": BF16_VARIANT_AUTO, "stream": BF16_VARIANT_STREAM,
+                 "scalar": BF16_VARIANT_SCALAR}
 
 GROUP = 128
 MAX_PROJ = 8
@@ -259,3 +270,38 @@ def gemv_multi(weights, scales, x, Ns, K: int, M: int = 1, ys=None, prepacked: b
                                            K, M, int(prepacked), _stream(stream))
     _check(rc, "cudalm_w4a16_gemv_bf16_multi")
     return ys
+
+
+# ---------------------------------------------------------------------------
+# bf16 GEMV (tied LM head), include/cudalm_bf16_gemv.h
+# ---------------------------------------------------------------------------
+
+def bf16_gemv_ptr(w: int, x: int, y: int, N: int, K: int, M: int,
+                  variant: int = BF16_VARIANT_AUTO, stream: int | None = None) -> int:
+    return _lib.cudalm_bf16_gemv_variant(w, x, y, N, K, M, variant, stream)
+
+
+def bf16_gemv_any(weight, x, N: int, K: int, M: int = 1, y=None,
+                  variant: int | str = BF16_VARIANT_AUTO, stream=None):
+    """y[M, N] = weight[N, K] bf16 @ x[M, K] bf16 (fp32 accumulation)."""
+    if isinstance(variant, str):
+        variant = BF16_VARIANTS[variant]
+    y = _out(y, M, N, x)
+    rc = _lib.cudalm_bf16_gemv_variant(_ptr(weight), _ptr(x), _ptr(y), N, K, M, variant,
+                                       _stream(stream))
+    _check(rc, "cudalm_bf16_gemv")
+    return y
+
+
+def bf16_gemv(weight, x, y, N: int, K: int, stream=None):
+    """Reference name and argument order (bf16_gemv.h:37-38)."""
+    return bf16_gemv_any(weight, x, N, K, 1, y=y, stream=stream)
+
+
+def batch_bf16_gemv(weight, x, y, N: int, K: int, B: int, stream=None):
+    """Reference name and argument order (batch_decode.h:77-79)."""
+    return bf16_gemv_any(weight, x, N, K, B, y=y, stream=stream)
+
+
+def bf16_gemv_kernel_regs(variant: int = BF16_VARIANT_STREAM) -> int:
+    return _lib.cudalm_bf16_gemv_kernel_regs(variant)

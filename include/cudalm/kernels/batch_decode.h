@@ -25,5 +25,12 @@ void batch_int4_gemv_bf16(const std::uint8_t* weight, const __half* scale,
 // Register count (VGPR + AGPR) of the small-M kernel; -1 if unavailable.
 int batch_int4_gemv_bf16_rowtile4_regs();
 
+// bf16 GEMV (tied LM head), B rows: y_b = W * x_b, x bf16 [B, K], y bf16
+// [B, N] (reference: include/cudalm/kernels/batch_decode.h:69-79). The
+// weight is streamed once for up to 32 rows; row b is bit-identical to
+// bf16_gemv on x_b alone. Any K >= 1 and 2-byte aligned bases.
+void batch_bf16_gemv(const __hip_bfloat16* weight, const __hip_bfloat16* x,
+                     __hip_bfloat16* y, int N, int K, int B, hipStream_t stream);
+
 }  // namespace kernels
 }  // namespace cudalm

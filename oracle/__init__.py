@@ -51,6 +51,12 @@ _SIGS = {
     "orc_time_gemv_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int],
                            ctypes.c_double),
     "orc_hardware_threads": ([], ctypes.c_int),
+    "orc_bf16_fixture": ([ctypes.c_uint32, _I64, _I64, _P, _P], None),
+    "orc_bf16_gemv": ([_P, _P, _P, _I64, _I64, _I64], None),
+    "orc_bf16_gemv_mt": ([_P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
+    "orc_bf16_gemv_f64": ([_P, _P, _P, _P, _I64, _I64, _I64], None),
+    "orc_time_bf16_gemv": ([_P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int],
+                           ctypes.c_double),
 }
 for _n, (_a, _r) in _SIGS.items():
     _f = getattr(_lib, _n)
@@ -233,6 +239,44 @@ def check_tolerance(y_bits, W, S, X, N, K, M, ulps: float = 2.0):
     """Pass iff |y - r| <= ulps * ulp_bf16(r) + CANCEL_FLOOR * sum|terms|,
     r = fp64 sum of the exact fp32 terms. Returns (ok, stats dict)."""
     r, a = gemv_f64(W, S, X, N, K, M)
+    return check_tolerance_f64(y_bits, r, a, M, N, ulps)
+
+
+# ---- bf16 GEMV (tied LM head) ----------------------------------------------
+
+def bf16_fixture(seed: int, N: int, K: int):
+    """test_bf16_gemv.cpp:44-57: (W bf16 bits [N, K], x bf16 bits [1, K])."""
+    W = np.empty((N, K), np.uint16)
+    X = np.empty((1, K), np.uint16)
+    _lib.orc_bf16_fixture(seed, N, K, _p(W), _p(X))
+    return W, X
+
+
+def bf16_gemv(W, X, N: int, K: int, M: int = 1, nthreads: int = 1) -> np.ndarray:
+    """ref_gemv_bf16 of test_bf16_gemv.cpp:62-73, M rows: bf16 bits [M, N]."""
+    Y = np.empty((M, N), np.uint16)
+    if nthreads > 1:
+        _lib.orc_bf16_gemv_mt(_p(W), _p(X), _p(Y), N, K, M, nthreads)
+    else:
+        _lib.orc_bf16_gemv(_p(W), _p(X), _p(Y), N, K, M)
+    return Y
+
+
+def bf16_gemv_f64(W, X, N: int, K: int, M: int = 1):
+    Y = np.empty((M, N), np.float64)
+    A = np.empty((M, N), np.float64)
+    _lib.orc_bf16_gemv_f64(_p(W), _p(X), _p(Y), _p(A), N, K, M)
+    return Y, A
+
+
+def time_bf16_gemv(W, X, N, K, M, nthreads, iters) -> float:
+    Y = np.empty((M, N), np.uint16)
+    return _lib.orc_time_bf16_gemv(_p(W), _p(X), _p(Y), N, K, M, nthreads, iters)
+
+
+def check_tolerance_f64(y_bits, r, a, M, N, ulps: float = 2.0):
+    """Pass iff |y - r| <= ulps * ulp_bf16(r) + CANCEL_FLOOR * a for the exact
+    sum r and the magnitude sum a. Returns (ok, stats dict)."""
     y = bf16_to_f32(np.asarray(y_bits, np.uint16).reshape(M, N)).astype(np.float64)
     err = np.abs(y - r)
     tol = ulps * bf16_ulp(r) + CANCEL_FLOOR * a
@@ -246,6 +290,11 @@ def check_tolerance(y_bits, W, S, X, N, K, M, ulps: float = 2.0):
         "n": int(err.size),
     }
     return not bad.any(), stats
+
+
+def check_bf16_tolerance(y_bits, W, X, N, K, M, ulps: float = 2.0):
+    r, a = bf16_gemv_f64(W, X, N, K, M)
+    return check_tolerance_f64(y_bits, r, a, M, N, ulps)
 
 
 # ---- the reference's own comparator (oracle/_ref) ---------------------------

@@ -85,6 +85,20 @@ int orc_synth_w4a16(uint64_t seed, float sigma, int64_t N, int64_t K,
                     uint8_t* W, uint16_t* S);
 void orc_synth_act_bf16(uint64_t seed, int64_t M, int64_t K, uint16_t* X);
 
+/* ---- bf16 GEMV (tied LM head), bf16_oracle.c --------------------------- */
+void orc_bf16_fixture(uint32_t seed, int64_t N, int64_t K, uint16_t* W, uint16_t* X);
+void orc_bf16_gemv(const uint16_t* W, const uint16_t* X, uint16_t* Y, int64_t N,
+                   int64_t K, int64_t M);
+void orc_bf16_gemv_rows(const uint16_t* W, const uint16_t* X, uint16_t* Y,
+                        int64_t N, int64_t K, int64_t M, int64_t n0, int64_t n1);
+void orc_bf16_gemv_mt(const uint16_t* W, const uint16_t* X, uint16_t* Y,
+                      int64_t N, int64_t K, int64_t M, int nthreads);
+void orc_bf16_gemv_f64(const uint16_t* W, const uint16_t* X, double* Y,
+                       double* Yabs, int64_t N, int64_t K, int64_t M);
+double orc_time_bf16_gemv(const uint16_t* W, const uint16_t* X, uint16_t* Y,
+                          int64_t N, int64_t K, int64_t M, int nthreads,
+                          int iters);
+
 /* ---- timing helper for the CPU baseline --------------------------------- */
 double orc_time_gemv_bf16(const uint8_t* W, const uint16_t* S,
                           const uint16_t* X, uint16_t* Y, int64_t N, int64_t K,

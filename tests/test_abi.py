@@ -13,17 +13,19 @@ import numpy as np
 import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(REPO, "include", "cudalm_w4a16.h")
+HEADERS = [os.path.join(REPO, "include", h) for h in ("cudalm_w4a16.h", "cudalm_bf16_gemv.h")]
 
 
 def declared_symbols():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"\b(cudalm_w4a16_\w+)\s*\(", text)))
+    syms = set()
+    for h in HEADERS:
+        syms |= set(re.findall(r"\b(cudalm_(?:w4a16|bf16)_\w+)\s*\(", open(h).read()))
+    return sorted(syms)
 
 
 def test_library_exports_every_declared_symbol(w4):
     syms = declared_symbols()
-    assert len(syms) >= 10
+    assert len(syms) >= 13
     for s in syms:
         assert hasattr(w4.lib(), s), s
     assert set(syms) == set(w4.EXPORTED_SYMBOLS)
@@ -53,6 +55,24 @@ def test_shape_preconditions_rejected_before_device(w4):
     # misaligned bases are legal for the file-layout entry, but not with a
     # vectorized variant forced
     assert w4.gemv_ptr(fake + 1, fake, fake, fake, 4, 128, 1, w4.VARIANT_STREAM) == w4.EVARIANT
+
+
+def test_bf16_gemv_preconditions_rejected_before_device(w4):
+    # include/cudalm_bf16_gemv.h: N, K, M >= 1; 2-byte aligned bases; a
+    # forced stream variant needs K % 8 == 0 and 16 B bases
+    fake = 0x1000
+    p = w4.bf16_gemv_ptr
+    assert p(fake, fake, fake, 0, 8, 1) == w4.EINVAL
+    assert p(fake, fake, fake, 4, 0, 1) == w4.EINVAL
+    assert p(fake, fake, fake, 4, 8, 0) == w4.EINVAL
+    assert p(None, fake, fake, 4, 8, 1) == w4.ENULL
+    assert p(fake, fake, None, 4, 8, 1) == w4.ENULL
+    assert p(fake + 1, fake, fake, 4, 8, 1) == w4.EALIGN
+    assert p(fake, fake, fake + 1, 4, 8, 1) == w4.EALIGN
+    assert p(fake, fake, fake, 4, 12, 1, w4.BF16_VARIANT_STREAM) == w4.EVARIANT
+    assert p(fake + 2, fake, fake, 4, 16, 1, w4.BF16_VARIANT_STREAM) == w4.EVARIANT
+    assert p(fake, fake, fake, 4, 16, 1, 7) == w4.EVARIANT
+    assert p(fake, fake, fake, 1 << 30, 16, 1) == w4.ERANGE
 
 
 def test_packed_bytes(w4):
@@ -95,12 +115,19 @@ def test_cpp_headers_compile_and_link(tmp_path, w4):
     src.write_text(r'''
 #include "cudalm/kernels/int4_gemv_bf16.h"
 #include "cudalm/kernels/batch_decode.h"
+#include "cudalm/kernels/bf16_gemv.h"
 #include "cudalm/w4a16_linear.h"
+#include "cudalm_bf16_gemv.h"
 #include "cudalm_w4a16.h"
 #include <cstdio>
 int main() {
   std::printf("%zu %zu\n", cudalm::packed_w4a16_bytes(16, 128), cudalm_w4a16_packed_bytes(32, 256));
-  return 0;
+  // the reference-named bf16 entry points resolve at link time
+  void (*f1)(const __hip_bfloat16*, const __hip_bfloat16*, __hip_bfloat16*, int, int, hipStream_t) =
+      cudalm::bf16_gemv;
+  void (*f2)(const __hip_bfloat16*, const __hip_bfloat16*, __hip_bfloat16*, int, int, int,
+             hipStream_t) = cudalm::kernels::batch_bf16_gemv;
+  return (f1 && f2) ? 0 : 1;
 }
 ''')
     exe = tmp_path / "use"
@@ -132,6 +159,26 @@ int main() {
     res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert res.returncode != 0
     assert "invalid shape" in res.stderr
+
+
+def test_cpp_bf16_entry_aborts_on_precondition(tmp_path, w4):
+    src = tmp_path / "bad_bf16.cpp"
+    src.write_text(r'''
+#include "cudalm/kernels/bf16_gemv.h"
+int main() {
+  // N < 1: the reference aborts (bf16_gemv.cu:113-114)
+  cudalm::bf16_gemv(nullptr, nullptr, nullptr, 0, 1024, nullptr);
+  return 0;
+}
+''')
+    exe = tmp_path / "bad_bf16"
+    libdir = os.path.dirname(w4.LIB_PATH)
+    cmd = ["/opt/rocm/bin/hipcc", "-std=c++17", "-I", os.path.join(REPO, "include"), str(src),
+           "-L", libdir, "-lcudalm_w4a16", f"-Wl,-rpath,{libdir}", "-o", str(exe)]
+    assert subprocess.run(cmd, capture_output=True).returncode == 0
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert res.returncode != 0
+    assert "bf16_gemv" in res.stderr and "invalid shape" in res.stderr
 
 
 def test_python_layer_raises_on_bad_shape(w4):
