@@ -6,6 +6,7 @@
 //   cudalm::kernels::batch_int4_gemv_bf16 include/cudalm/kernels/batch_decode.h:61-67
 //   cudalm::bf16_gemv                     include/cudalm/kernels/bf16_gemv.h:37-38
 //   cudalm::kernels::batch_bf16_gemv      include/cudalm/kernels/batch_decode.h:77-79
+//   cudalm::kernels::qwen35_silu_mul_bf16 include/cudalm/kernels/qwen35_kernels.h:146-155
 //   CUDALM_PRECONDITION / CUDA_CHECK_LAUNCH (abort)  include/cudalm/cuda_check.h:38-63
 
 #include <cstdio>
@@ -15,6 +16,7 @@
 #include "cudalm/kernels/batch_decode.h"
 #include "cudalm/kernels/bf16_gemv.h"
 #include "cudalm/kernels/int4_gemv_bf16.h"
+#include "cudalm/kernels/swiglu.h"
 #include "cudalm/w4a16_linear.h"
 #include "cudalm_bf16_gemv.h"
 #include "cudalm_w4a16.h"
@@ -102,6 +104,25 @@ void w4a16_forward_bf16(const PackedW4A16Linear& lin, const __hip_bfloat16* x, _
               cudalm_w4a16_gemv_bf16_prepacked(lin.packed, bits(x), bits(y), lin.N, lin.K, M,
                                                stream));
 }
+
+void w4a16_swiglu_forward_bf16(const PackedW4A16Linear& gate, const PackedW4A16Linear& up,
+                               const __hip_bfloat16* x, __hip_bfloat16* y, int M,
+                               hipStream_t stream) {
+  W4A16_CHECK("w4a16_swiglu_forward_bf16",
+              (gate.N != up.N || gate.K != up.K)
+                  ? CUDALM_W4A16_EINVAL
+                  : cudalm_w4a16_swiglu_bf16(gate.packed, nullptr, up.packed, nullptr, bits(x),
+                                             bits(y), gate.N, gate.K, M, 1, stream));
+}
+
+namespace kernels {
+
+void qwen35_silu_mul_bf16(const __hip_bfloat16* gate, const __hip_bfloat16* up,
+                          __hip_bfloat16* y, std::size_t n, hipStream_t stream) {
+  W4A16_CHECK("qwen35_silu_mul_bf16", cudalm_silu_mul_bf16(bits(gate), bits(up), bits(y), n, stream));
+}
+
+}  // namespace kernels
 
 }  // namespace cudalm
 

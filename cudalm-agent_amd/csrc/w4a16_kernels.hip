@@ -440,6 +440,114 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// SwiGLU epilogue: the MLP's gate and up projections share x, and the down
+// projection consumes silu(gate) * up (reference: src/runtime/
+// qwen35_deltanet.cpp:236-251, src/kernels/qwen35_kernels.cu:458-476).
+// ---------------------------------------------------------------------------
+
+// y = bf16( f32(bf16(g / (1 + exp(-g)))) * u ) on bf16 inputs g, u: SiLU in
+// fp32, rounded to bf16 first, then the product rounded once
+// (include/cudalm/kernels/qwen35_kernels.h:146-152).
+__device__ __forceinline__ uint32_t silu_mul_bits(uint32_t g_bits, uint32_t u_bits) {
+  const float g = bf16_lo(g_bits);
+  const float s = bf16_lo(f32_to_bf16_rne(g / (1.0f + expf(-g))));
+  return f32_to_bf16_rne(s * bf16_lo(u_bits));
+}
+
+// Element-wise silu(gate) * up over n values; 8 per thread (16 B vectors
+// when the three bases are 16 B aligned, element-wise otherwise).
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gate,
+                                                       const uint16_t* __restrict__ up,
+                                                       uint16_t* __restrict__ y, size_t n,
+                                                       int vec) {
+  const size_t e0 = (static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  if (e0 >= n) return;
+  if (vec && e0 + 8 <= n) {
+    const u32x4_t g = *reinterpret_cast<const u32x4_t*>(gate + e0);
+    const u32x4_t u = *reinterpret_cast<const u32x4_t*>(up + e0);
+    u32x4_t o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      o[q] = silu_mul_bits(g[q] & 0xFFFFu, u[q] & 0xFFFFu) |
+             (silu_mul_bits(g[q] >> 16, u[q] >> 16) << 16);
+    *reinterpret_cast<u32x4_t*>(y + e0) = o;
+  } else {
+    const size_t e1 = e0 + 8 < n ? e0 + 8 : n;
+    for (size_t e = e0; e < e1; ++e) y[e] = static_cast<uint16_t>(silu_mul_bits(gate[e], up[e]));
+  }
+}
+
+// gate and up W4A16 projections of the same x (P.count == 2, equal N, gate
+// first) with the SwiGLU epilogue, one launch. Work is split like the split
+// kernel: a workgroup takes TPR = max(1, 4 / (2U)) row tiles; each tile's
+// 2U unit partials (U of gate, then U of up) are computed on separate waves
+// and summed in unit order per projection, so gate and up carry exactly the
+// bits of their single-projection calls before the epilogue. Activation
+// rows are processed in chunks of mc <= 16 * CT rows (blockIdx.y).
+template <bool PACKED, int NR, bool SVEC, int CT>
+__global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
+    const ProjTable P, const uint16_t* __restrict__ X, int K, int M, int mc) {
+  extern __shared__ u32x4_t xs[];
+  const int G = K >> 7;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int i = lane & 15, a = lane >> 4;
+  const int nt = P.tile_end[0];  // row tiles per projection
+  const int N = P.n[0];
+  const int U = (G + kUnit - 1) / kUnit;
+  const int TPR = 2 * U >= kStreamWaves ? 1 : kStreamWaves / (2 * U);
+  const int nslots = TPR * 2 * U;
+  const int t0 = blockIdx.x * TPR;
+  const int m0 = blockIdx.y * mc;
+  const int mrows = min(mc, M - m0);
+  const int pitch = (K >> 3) + 1;
+  f32x4_t* slots = reinterpret_cast<f32x4_t*>(
+      reinterpret_cast<float*>(xs + mrows * pitch) + G * 16 * CT);
+
+  // slot sl -> (row tile t0 + sl / 2U, projection (sl % 2U) / U, unit sl % U)
+  auto slot_load = [&](StreamUnit& u, int sl) {
+    const int tf = min(t0 + sl / (2 * U), nt - 1);
+    const int r = sl % (2 * U);
+    stream_load_t<PACKED, SVEC>(u, P, K, G, (r / U) * nt + tf, (r % U) * kUnit, lane);
+  };
+  StreamUnit cur;
+  slot_load(cur, min(wave, nslots - 1));
+  const u32x4_t* xrow[CT];
+  const float* corr =
+      stream_prologue<CT>(xs, xrow, X + static_cast<size_t>(m0) * K, K, mrows, wave, i, a);
+
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int sl = wave; sl < nslots; sl += kStreamWaves) {
+    if (sl != wave) slot_load(cur, sl);
+    f32x4_t part[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
+    const int g0 = (sl % U) * kUnit;
+    stream_unit<NR, CT>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) slots[(sl * CT + ct) * 64 + lane] = part[ct];
+  }
+  __syncthreads();
+  if (wave < TPR && t0 + wave < nt) {
+    const int n = (t0 + wave) * kTileRows + i;
+    const int base = wave * 2 * U;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      f32x4_t tg = zero, tu = zero;
+      for (int u = 0; u < U; ++u) tg = tg + slots[((base + u) * CT + ct) * 64 + lane];
+      for (int u = 0; u < U; ++u) tu = tu + slots[((base + U + u) * CT + ct) * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int m = ct * 16 + 4 * a + r;
+        if (m < mrows && n < N)
+          P.y[0][static_cast<size_t>(m0 + m) * N + n] = static_cast<uint16_t>(
+              silu_mul_bits(f32_to_bf16_rne(16.0f * tg[r]), f32_to_bf16_rne(16.0f * tu[r])));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Tile kernel: any M. A workgroup of WN x WM waves owns a (WN*RB*16) x
 // (WM*CT*16) output tile (n x m); K is walked in chunks of GPC groups whose
 // activations are staged in LDS; each wave preloads the chunk's weights.
@@ -944,6 +1052,51 @@ int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStrea
   return launch_status();
 }
 
+size_t swiglu_lds_bytes(int K, int mrows) {
+  const int CT = mrows > 16 ? 2 : 1;
+  const int U = (K / kGroup + kUnit - 1) / kUnit;
+  const int tpr = 2 * U >= kStreamWaves ? 1 : kStreamWaves / (2 * U);
+  return stream_lds_bytes(K, mrows) + static_cast<size_t>(tpr) * 2 * U * CT * 64 * 16;
+}
+
+template <bool PACKED, int NR, bool SVEC, int CT>
+int launch_swiglu_t(const ProjTable& P, const uint16_t* X, int K, int M, int mc,
+                    hipStream_t stream) {
+  const size_t lds = swiglu_lds_bytes(K, mc);
+  const int U = (K / kGroup + kUnit - 1) / kUnit;
+  const int tpr = 2 * U >= kStreamWaves ? 1 : kStreamWaves / (2 * U);
+  const int gx = (P.tile_end[0] + tpr - 1) / tpr;
+  const int gy = (M + mc - 1) / mc;
+  if (gy > 65535) return CUDALM_W4A16_ERANGE;
+  auto kern = w4a16_swiglu_kernel<PACKED, NR, SVEC, CT>;
+  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+  hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(kStreamWaves * 64), lds, stream, P, X, K, M, mc);
+  return launch_status();
+}
+
+// Activation rows per chunk of the fused kernel: up to 32 when M > 16, as
+// many as the LDS holds; 0 if not even one row fits.
+int swiglu_rows_per_chunk(int K, int M) {
+  int mc = M > 16 ? 32 : M;
+  while (mc > 0 && swiglu_lds_bytes(K, mc) > kLdsMax) --mc;
+  return mc;
+}
+
+template <bool PACKED>
+int launch_swiglu(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
+  const int G = K / kGroup;
+  const bool svec = !PACKED && G % 8 == 0 && aligned(P.s[0], 16) && aligned(P.s[1], 16);
+  const int mc = swiglu_rows_per_chunk(K, M);
+  if (mc < 1) return CUDALM_W4A16_ERANGE;
+#define W4A16_SWIGLU(NR, CT)                                                       \
+  (svec ? launch_swiglu_t<PACKED, NR, true, CT>(P, X, K, M, mc, stream)           \
+        : launch_swiglu_t<PACKED, NR, false, CT>(P, X, K, M, mc, stream))
+  if (mc > 16) return W4A16_SWIGLU(4, 2);
+  if (M == 1) return W4A16_SWIGLU(1, 1);
+  return W4A16_SWIGLU(4, 1);
+#undef W4A16_SWIGLU
+}
+
 // Unit-parallel (split) when the tiles alone leave most of the machine
 // idle and each tile has several units; otherwise tile-serial streaming.
 bool prefer_split(const ProjTable& P, int K, int M) {
@@ -1221,6 +1374,48 @@ int cudalm_w4a16_gemv_bf16_multi(const cudalm_w4a16_proj* projs, int count, cons
   return prepacked ? launch_stream<true>(P, x, K, M, stream) : launch_stream<false>(P, x, K, M, stream);
 }
 
+int cudalm_silu_mul_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* y, size_t n,
+                         hipStream_t stream) {
+  if (n == 0) return CUDALM_W4A16_OK;
+  if (!gate || !up || !y) return CUDALM_W4A16_ENULL;
+  if (!aligned(gate, 2) || !aligned(up, 2) || !aligned(y, 2)) return CUDALM_W4A16_EALIGN;
+  const size_t threads = (n + 7) / 8;
+  const size_t blocks = (threads + 255) / 256;
+  if (blocks > 0x7FFFFFFFu) return CUDALM_W4A16_ERANGE;
+  const int vec = aligned(gate, 16) && aligned(up, 16) && aligned(y, 16);
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                     gate, up, y, n, vec);
+  return launch_status();
+}
+
+int cudalm_w4a16_swiglu_bf16(const void* gate_weight, const uint16_t* gate_scale,
+                             const void* up_weight, const uint16_t* up_scale, const uint16_t* x,
+                             uint16_t* y, int N, int K, int M, int prepacked,
+                             hipStream_t stream) {
+  if (int rc = check_shape(N, K, M)) return rc;
+  if (!gate_weight || !up_weight || !x || !y || (!prepacked && (!gate_scale || !up_scale)))
+    return CUDALM_W4A16_ENULL;
+  if (static_cast<long long>((N + kTileRows - 1) / kTileRows) * 2 > (1LL << 30))
+    return CUDALM_W4A16_ERANGE;
+  const bool vec_ok = aligned(gate_weight, 16) && aligned(up_weight, 16) && aligned(x, 16) &&
+                      aligned(y, 2) &&
+                      (prepacked || (aligned(gate_scale, 2) && aligned(up_scale, 2)));
+  if (!vec_ok) return CUDALM_W4A16_EALIGN;
+  ProjTable P = {};
+  const int nt = (N + kTileRows - 1) / kTileRows;
+  P.w[0] = static_cast<const uint8_t*>(gate_weight);
+  P.s[0] = gate_scale;
+  P.w[1] = static_cast<const uint8_t*>(up_weight);
+  P.s[1] = up_scale;
+  P.y[0] = P.y[1] = y;
+  P.n[0] = P.n[1] = N;
+  P.tile_end[0] = nt;
+  P.tile_end[1] = 2 * nt;
+  P.count = 2;
+  return prepacked ? launch_swiglu<true>(P, x, K, M, stream)
+                   : launch_swiglu<false>(P, x, K, M, stream);
+}
+
 int cudalm_w4a16_dequant_f32(const uint8_t* weight, const uint16_t* scale, int8_t* q_out,
                              float* w_out, int N, int K, hipStream_t stream) {
   if (int rc = check_shape(N, K, 1)) return rc;
@@ -1244,6 +1439,7 @@ int cudalm_w4a16_kernel_regs(int variant) {
     case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_gemm_kernel<2, 2, 2, 2, 2, true>);
     case CUDALM_W4A16_VARIANT_BYTEWISE: return regs_of(w4a16_bytewise_kernel);
     case CUDALM_W4A16_VARIANT_SPLIT: return regs_of(w4a16_split_kernel<true, 1, false, 1>);
+    case CUDALM_W4A16_VARIANT_SWIGLU: return regs_of(w4a16_swiglu_kernel<true, 1, false, 1>);
     default: return -1;
   }
 }

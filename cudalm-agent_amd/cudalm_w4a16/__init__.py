@@ -48,6 +48,8 @@ _SIGS = {
     "cudalm_w4a16_dequant_f32": ([_P, _P, _P, _P, _I, _I, _P], _I),
     "cudalm_w4a16_gemv_bf16_multi": ([_P, _I, _P, _I, _I, _I, _P], _I),
     "cudalm_w4a16_kernel_regs": ([_I], _I),
+    "cudalm_w4a16_swiglu_bf16": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P], _I),
+    "cudalm_silu_mul_bf16": ([_P, _P, _P, _SZ, _P], _I),
     "cudalm_bf16_gemv": ([_P, _P, _P, _I, _I, _I, _P], _I),
     "cudalm_bf16_gemv_variant": ([_P, _P, _P, _I, _I, _I, _I, _P], _I),
     "cudalm_bf16_gemv_kernel_regs": ([_I], _I),
@@ -74,6 +76,7 @@ VARIANT_TILE32 = 3
 VARIANT_PREFILL = 4
 VARIANT_BYTEWISE = 5
 VARIANT_SPLIT = 6
+VARIANT_SWIGLU = 7  # kernel_regs only
 VARIANTS = {
     "split": VARIANT_SPLIT,
     "auto": VARIANT_AUTO,
@@ -270,6 +273,28 @@ def gemv_multi(weights, scales, x, Ns, K: int, M: int = 1, ys=None, prepacked: b
                                            K, M, int(prepacked), _stream(stream))
     _check(rc, "cudalm_w4a16_gemv_bf16_multi")
     return ys
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU: fused gate/up + silu*mul, and the element-wise stage
+# ---------------------------------------------------------------------------
+
+def swiglu(gate_w, gate_s, up_w, up_s, x, N: int, K: int, M: int = 1, y=None,
+           prepacked: bool = False, stream=None):
+    """y[M, N] = silu(gate(x)) * up(x), one launch (bf16 roundings of the
+    reference's gate -> up -> qwen35_silu_mul_bf16 sequence)."""
+    y = _out(y, M, N, x)
+    rc = _lib.cudalm_w4a16_swiglu_bf16(_ptr(gate_w), _ptr(gate_s), _ptr(up_w), _ptr(up_s),
+                                       _ptr(x), _ptr(y), N, K, M, int(prepacked), _stream(stream))
+    _check(rc, "cudalm_w4a16_swiglu_bf16")
+    return y
+
+
+def qwen35_silu_mul_bf16(gate, up, y, n: int, stream=None):
+    """Reference name and argument order (qwen35_kernels.h:146-155)."""
+    rc = _lib.cudalm_silu_mul_bf16(_ptr(gate), _ptr(up), _ptr(y), n, _stream(stream))
+    _check(rc, "cudalm_silu_mul_bf16")
+    return y
 
 
 # ---------------------------------------------------------------------------

@@ -46,4 +46,12 @@ void repack_w4a16_host(const std::uint8_t* weight, const std::uint16_t* scale,
 void w4a16_forward_bf16(const PackedW4A16Linear& lin, const __hip_bfloat16* x,
                         __hip_bfloat16* y, int M, hipStream_t stream);
 
+// y[M, N] = silu(gate(x)) * up(x) with the reference's roundings (gate and
+// up outputs as bf16, SiLU rounded to bf16, then the product), one launch;
+// equal to w4a16_forward_bf16 on each projection followed by
+// kernels::qwen35_silu_mul_bf16. gate and up must share N and K.
+void w4a16_swiglu_forward_bf16(const PackedW4A16Linear& gate, const PackedW4A16Linear& up,
+                               const __hip_bfloat16* x, __hip_bfloat16* y, int M,
+                               hipStream_t stream);
+
 }  // namespace cudalm

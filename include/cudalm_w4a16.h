@@ -112,6 +112,31 @@ int cudalm_w4a16_gemv_bf16_multi(const cudalm_w4a16_proj* projs, int count,
                                  const uint16_t* x, int K, int M, int prepacked,
                                  hipStream_t stream);
 
+/* SwiGLU MLP front half in one launch: the gate and up projections of the
+ * same x[M, K] (both [N, K], file layout with scales or both prepacked)
+ * and the epilogue
+ *   y[m, n] = bf16( f32(bf16(silu(g))) * f32(u) ),  silu(g) = g / (1 + exp(-g))
+ * on g = gate(x)[m, n] and u = up(x)[m, n] as bf16. g and u carry exactly
+ * the bits of cudalm_w4a16_gemv_bf16 on each projection, and the epilogue
+ * is cudalm_silu_mul_bf16's, so y equals the reference's three-step
+ * sequence gate -> up -> qwen35_silu_mul_bf16
+ * (src/runtime/qwen35_deltanet.cpp:236-247) run on this library, with no
+ * intermediate buffers. Any M (processed in chunks of up to 32 rows); all
+ * bases 16 B aligned (y: 2 B), else EALIGN. No counterpart in the
+ * reference. */
+int cudalm_w4a16_swiglu_bf16(const void* gate_weight, const uint16_t* gate_scale,
+                             const void* up_weight, const uint16_t* up_scale,
+                             const uint16_t* x, uint16_t* y, int N, int K, int M,
+                             int prepacked, hipStream_t stream);
+
+/* y[i] = bf16( f32(bf16(silu(f32(gate[i])))) * f32(up[i]) ) for i < n, bf16
+ * bit patterns. Replaces kernels::qwen35_silu_mul_bf16
+ * (include/cudalm/kernels/qwen35_kernels.h:146-154); any n and 2-byte
+ * aligned bases (the reference requires n % 8 == 0 and 16 B bases). SiLU is
+ * evaluated in fp32 with a correctly rounded divide and the device expf. */
+int cudalm_silu_mul_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* y,
+                         size_t n, hipStream_t stream);
+
 /* Dequantize through the kernels' own nibble decoder: q_out[N, K] int8 and
  * w_out[N, K] = q * f32(scale) (either output may be NULL). The weight base
  * must be 4 B aligned. Equivalent to the reference's dequant_reference
@@ -132,6 +157,7 @@ int cudalm_w4a16_dequant_f32(const uint8_t* weight, const uint16_t* scale,
 #define CUDALM_W4A16_VARIANT_PREFILL 4  /* 64x64 per wave, 128x128 per group */
 #define CUDALM_W4A16_VARIANT_BYTEWISE 5 /* misaligned-base fallback */
 #define CUDALM_W4A16_VARIANT_SPLIT 6    /* M <= 32, units of a tile on separate waves */
+#define CUDALM_W4A16_VARIANT_SWIGLU 7   /* kernel_regs only: the fused SwiGLU kernel */
 int cudalm_w4a16_gemv_bf16_variant(const uint8_t* weight, const uint16_t* scale,
                                    const uint16_t* x, uint16_t* y, int N, int K,
                                    int M, int variant, hipStream_t stream);

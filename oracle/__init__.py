@@ -51,6 +51,8 @@ _SIGS = {
     "orc_time_gemv_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int],
                            ctypes.c_double),
     "orc_hardware_threads": ([], ctypes.c_int),
+    "orc_silu_bf16": ([ctypes.c_uint16], ctypes.c_uint16),
+    "orc_silu_mul_bf16": ([_P, _P, _P, ctypes.c_size_t], None),
     "orc_bf16_fixture": ([ctypes.c_uint32, _I64, _I64, _P, _P], None),
     "orc_bf16_gemv": ([_P, _P, _P, _I64, _I64, _I64], None),
     "orc_bf16_gemv_mt": ([_P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
@@ -240,6 +242,23 @@ def check_tolerance(y_bits, W, S, X, N, K, M, ulps: float = 2.0):
     r = fp64 sum of the exact fp32 terms. Returns (ok, stats dict)."""
     r, a = gemv_f64(W, S, X, N, K, M)
     return check_tolerance_f64(y_bits, r, a, M, N, ulps)
+
+
+# ---- SwiGLU element-wise stage ---------------------------------------------
+
+def silu_bf16(g_bits) -> np.ndarray:
+    g = np.ascontiguousarray(g_bits, np.uint16)
+    return np.array([_lib.orc_silu_bf16(int(v)) for v in g.ravel()], np.uint16).reshape(g.shape)
+
+
+def silu_mul_bf16(gate, up) -> np.ndarray:
+    """qwen35_silu_mul_kernel (qwen35_kernels.cu:458-476) on bf16 bit arrays."""
+    g = np.ascontiguousarray(gate, np.uint16)
+    u = np.ascontiguousarray(up, np.uint16)
+    assert g.shape == u.shape
+    y = np.empty(g.shape, np.uint16)
+    _lib.orc_silu_mul_bf16(_p(g), _p(u), _p(y), g.size)
+    return y
 
 
 # ---- bf16 GEMV (tied LM head) ----------------------------------------------

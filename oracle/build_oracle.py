@@ -1,7 +1,7 @@
 """Build recipe for the CPU oracle (test infrastructure only).
 
   oracle/liborc_w4a16.so   plain-C restatement of the reference's CPU path
-                           (w4a16_oracle.c, bf16_oracle.c),
+                           (w4a16_oracle.c, bf16_oracle.c, swiglu_oracle.c),
                            gcc, -ffp-contract=off
   oracle/_ref/libref_stage_compare.so
                            the reference's own header-only fp16/bf16 decoders
@@ -37,6 +37,7 @@ def build_oracle() -> str:
     _run(["gcc", "-O2", "-std=c99", "-D_POSIX_C_SOURCE=200809L", "-fPIC", "-shared",
           "-ffp-contract=off", "-fno-fast-math", "-Wall",
           os.path.join(HERE, "w4a16_oracle.c"), os.path.join(HERE, "bf16_oracle.c"),
+          os.path.join(HERE, "swiglu_oracle.c"),
           "-o", tmp, "-lm", "-lpthread"])
     os.replace(tmp, ORACLE_LIB)
     return ORACLE_LIB

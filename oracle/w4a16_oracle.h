@@ -99,6 +99,10 @@ double orc_time_bf16_gemv(const uint16_t* W, const uint16_t* X, uint16_t* Y,
                           int64_t N, int64_t K, int64_t M, int nthreads,
                           int iters);
 
+/* ---- SwiGLU element-wise stage, swiglu_oracle.c ------------------------ */
+uint16_t orc_silu_bf16(uint16_t g_bits);
+void orc_silu_mul_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* y, size_t n);
+
 /* ---- timing helper for the CPU baseline --------------------------------- */
 double orc_time_gemv_bf16(const uint8_t* W, const uint16_t* S,
                           const uint16_t* X, uint16_t* Y, int64_t N, int64_t K,

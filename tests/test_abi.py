@@ -19,7 +19,7 @@ HEADERS = [os.path.join(REPO, "include", h) for h in ("cudalm_w4a16.h", "cudalm_
 def declared_symbols():
     syms = set()
     for h in HEADERS:
-        syms |= set(re.findall(r"\b(cudalm_(?:w4a16|bf16)_\w+)\s*\(", open(h).read()))
+        syms |= set(re.findall(r"\b(cudalm_[a-z0-9_]+)\s*\(", open(h).read()))
     return sorted(syms)
 
 
