@@ -1271,6 +1271,9 @@ const char* cudalm_w4a16_strerror(int code) {
     case CUDALM_W4A16_ELAUNCH: return "HIP kernel launch failed";
     case CUDALM_W4A16_ERANGE: return "shape exceeds the kernels' index range";
     case CUDALM_W4A16_EVARIANT: return "unknown or inapplicable kernel variant";
+    case -7: return "weight file breaks a .cudalm v2 container rule";
+    case -8: return "weight file could not be opened or mapped";
+    case -9: return "tensor not found, or not of the expected dtype / shape";
     default: return "unknown error code";
   }
 }

@@ -51,6 +51,17 @@ _SIGS = {
     "cudalm_w4a16_swiglu_bf16": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P], _I),
     "cudalm_silu_mul_bf16": ([_P, _P, _P, _SZ, _P], _I),
     "cudalm_bf16_gemv": ([_P, _P, _P, _I, _I, _I, _P], _I),
+    "cudalm_v2_open": ([ctypes.c_char_p, _P, ctypes.c_char_p, _SZ], _I),
+    "cudalm_v2_close": ([_P], None),
+    "cudalm_v2_num_tensors": ([_P], _I),
+    "cudalm_v2_tensor_at": ([_P, _I, _P], _I),
+    "cudalm_v2_find": ([_P, ctypes.c_char_p, _P], _I),
+    "cudalm_v2_meta": ([_P, ctypes.c_char_p], ctypes.c_char_p),
+    "cudalm_v2_get_config": ([_P, _P], _I),
+    "cudalm_v2_validate_layer": ([_P, _I, ctypes.c_char_p, _SZ], _I),
+    "cudalm_v2_w4a16_shape": ([_P, ctypes.c_char_p, _P, _P], _I),
+    "cudalm_v2_upload_w4a16_packed": ([_P, ctypes.c_char_p, _P, _SZ, _P], _I),
+    "cudalm_v2_upload": ([_P, ctypes.c_char_p, _P, _SZ, _P], _I),
     "cudalm_bf16_gemv_variant": ([_P, _P, _P, _I, _I, _I, _I, _P], _I),
     "cudalm_bf16_gemv_kernel_regs": ([_I], _I),
 }
@@ -68,6 +79,9 @@ EALIGN = -3
 ELAUNCH = -4
 ERANGE = -5
 EVARIANT = -6
+V2_EFORMAT = -7
+V2_EIO = -8
+V2_ENOTFOUND = -9
 
 VARIANT_AUTO = 0
 VARIANT_STREAM = 1
@@ -330,3 +344,126 @@ def batch_bf16_gemv(weight, x, y, N: int, K: int, B: int, stream=None):
 
 def bf16_gemv_kernel_regs(variant: int = BF16_VARIANT_STREAM) -> int:
     return _lib.cudalm_bf16_gemv_kernel_regs(variant)
+
+
+# ---------------------------------------------------------------------------
+# .cudalm v2 reader (include/cudalm_v2.h)
+# ---------------------------------------------------------------------------
+
+class V2Tensor(ctypes.Structure):
+    """struct cudalm_v2_tensor."""
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int), ("ndim", ctypes.c_int),
+                ("dims", ctypes.c_int64 * 8), ("offset", ctypes.c_uint64),
+                ("byte_size", ctypes.c_uint64), ("align", ctypes.c_int), ("host", ctypes.c_void_p)]
+
+    @property
+    def shape(self):
+        return tuple(self.dims[:self.ndim])
+
+    def bytes(self) -> bytes:
+        return ctypes.string_at(self.host, self.byte_size)
+
+
+_CFG_FIELDS = ("hidden_size", "num_hidden_layers", "intermediate_size", "vocab_size", "n_heads",
+               "n_kv_heads", "head_dim", "lin_num_k_heads", "lin_num_v_heads", "lin_key_head_dim",
+               "lin_value_head_dim", "lin_conv_kernel_dim", "full_attention_interval",
+               "group_size", "max_seq_len")
+
+
+class V2Config(ctypes.Structure):
+    """struct cudalm_v2_config."""
+    _fields_ = ([(n, ctypes.c_int32) for n in _CFG_FIELDS] +
+                [("eps", ctypes.c_float), ("rope_theta", ctypes.c_float),
+                 ("partial_rotary_factor", ctypes.c_float), ("mrope_section", ctypes.c_int32 * 3)])
+
+
+class V2FormatError(ValueError):
+    def __init__(self, code: int, reason: str):
+        self.code = code
+        self.reason = reason
+        super().__init__(f"{reason} (code {code})")
+
+
+class V2File:
+    """A validated, memory-mapped .cudalm v2 file (WeightFileV2's role,
+    weight_loader_v2.cpp:48-240)."""
+
+    def __init__(self, path: str):
+        self._h = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(512)
+        rc = _lib.cudalm_v2_open(os.fsencode(path), ctypes.byref(self._h), err, 512)
+        if rc != OK:
+            self._h = None
+            raise V2FormatError(rc, err.value.decode())
+
+    def close(self) -> None:
+        if self._h:
+            _lib.cudalm_v2_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        self.close()
+
+    def tensors(self):
+        out = []
+        for i in range(_lib.cudalm_v2_num_tensors(self._h)):
+            t = V2Tensor()
+            _check(_lib.cudalm_v2_tensor_at(self._h, i, ctypes.byref(t)), "cudalm_v2_tensor_at")
+            out.append(t)
+        return out
+
+    def find(self, name: str):
+        t = V2Tensor()
+        rc = _lib.cudalm_v2_find(self._h, name.encode(), ctypes.byref(t))
+        return t if rc == OK else None
+
+    def meta(self, key: str):
+        v = _lib.cudalm_v2_meta(self._h, key.encode())
+        return None if v is None else v.decode()
+
+    def config(self) -> V2Config:
+        c = V2Config()
+        _check(_lib.cudalm_v2_get_config(self._h, ctypes.byref(c)), "cudalm_v2_get_config")
+        return c
+
+    def validate_layer(self, idx: int):
+        """None if the layer's tensor set is complete, else the reason."""
+        err = ctypes.create_string_buffer(512)
+        rc = _lib.cudalm_v2_validate_layer(self._h, idx, err, 512)
+        return None if rc == OK else err.value.decode()
+
+    def w4a16_shape(self, prefix: str):
+        N, K = ctypes.c_int(), ctypes.c_int()
+        rc = _lib.cudalm_v2_w4a16_shape(self._h, prefix.encode(), ctypes.byref(N), ctypes.byref(K))
+        if rc != OK:
+            raise KeyError(prefix)
+        return N.value, K.value
+
+    def load_w4a16_packed(self, prefix: str, device="cuda", stream=None):
+        """Repack-at-load of one projection: (packed uint8 tensor, N, K)."""
+        import torch
+
+        N, K = self.w4a16_shape(prefix)
+        out = torch.empty(packed_bytes(N, K), dtype=torch.uint8, device=device)
+        rc = _lib.cudalm_v2_upload_w4a16_packed(self._h, prefix.encode(), _ptr(out), out.numel(),
+                                                _stream(stream))
+        _check(rc, "cudalm_v2_upload_w4a16_packed")
+        return out, N, K
+
+    def load_raw(self, name: str, device="cuda", stream=None):
+        """A tensor's file bytes on the device, as a uint8 tensor."""
+        import torch
+
+        t = self.find(name)
+        if t is None:
+            raise KeyError(name)
+        out = torch.empty(t.byte_size, dtype=torch.uint8, device=device)
+        rc = _lib.cudalm_v2_upload(self._h, name.encode(), _ptr(out), out.numel(), _stream(stream))
+        _check(rc, "cudalm_v2_upload")
+        return out

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(REPO, "include", h) for h in ("cudalm_w4a16.h", "cudalm_bf16_gemv.h")]
+HEADERS = [os.path.join(REPO, "include", h)
+           for h in ("cudalm_w4a16.h", "cudalm_bf16_gemv.h", "cudalm_v2.h")]
 
 
 def declared_symbols():
@@ -33,7 +34,7 @@ def test_library_exports_every_declared_symbol(w4):
 
 def test_version_and_strerror(w4):
     assert w4.version() >= 100
-    for code in range(-6, 1):
+    for code in range(-9, 1):
         assert w4.strerror(code)
     assert "unknown" in w4.strerror(-99)
 
@@ -118,6 +119,7 @@ def test_cpp_headers_compile_and_link(tmp_path, w4):
 #include "cudalm/kernels/bf16_gemv.h"
 #include "cudalm/w4a16_linear.h"
 #include "cudalm_bf16_gemv.h"
+#include "cudalm_v2.h"
 #include "cudalm_w4a16.h"
 #include <cstdio>
 int main() {
