@@ -4,6 +4,7 @@
 // Reference interfaces replaced here:
 //   cudalm::int4_gemv_bf16                include/cudalm/kernels/int4_gemv_bf16.h:46-52
 //   cudalm::kernels::batch_int4_gemv_bf16 include/cudalm/kernels/batch_decode.h:61-67
+//   cudalm::int4_gemv                     include/cudalm/kernels/int4_gemv.h:22-40
 //   cudalm::bf16_gemv                     include/cudalm/kernels/bf16_gemv.h:37-38
 //   cudalm::kernels::batch_bf16_gemv      include/cudalm/kernels/batch_decode.h:77-79
 //   cudalm::kernels::qwen35_silu_mul_bf16 include/cudalm/kernels/qwen35_kernels.h:146-155
@@ -15,6 +16,7 @@
 
 #include "cudalm/kernels/batch_decode.h"
 #include "cudalm/kernels/bf16_gemv.h"
+#include "cudalm/kernels/int4_gemv.h"
 #include "cudalm/kernels/int4_gemv_bf16.h"
 #include "cudalm/kernels/swiglu.h"
 #include "cudalm/w4a16_linear.h"
@@ -44,8 +46,15 @@ const std::uint16_t* bits(const __hip_bfloat16* p) {
   return reinterpret_cast<const std::uint16_t*>(p);
 }
 std::uint16_t* bits(__hip_bfloat16* p) { return reinterpret_cast<std::uint16_t*>(p); }
+std::uint16_t* bits(__half* p) { return reinterpret_cast<std::uint16_t*>(p); }
 
 }  // namespace
+
+void int4_gemv(const std::uint8_t* weight, const __half* scales, const __half* x, __half* y,
+               int N, int K, hipStream_t stream) {
+  W4A16_CHECK("int4_gemv",
+              cudalm_w4a16_gemv_f16(weight, bits(scales), bits(x), bits(y), N, K, 1, stream));
+}
 
 void bf16_gemv(const __hip_bfloat16* weight, const __hip_bfloat16* x, __hip_bfloat16* y, int N,
                int K, hipStream_t stream) {

@@ -117,6 +117,55 @@ __device__ __forceinline__ f32x4_t group_product(u32x4_t w, const u32x4_t (&xa)[
   return t;
 }
 
+// Activation / output element type of a kernel instance. Both encode a
+// weight nibble as the exact value 1.5 + q/16 in the activation's 16-bit
+// format, so the same offset cancellation and epilogue apply.
+struct ActBf16 {
+  static constexpr uint32_t kNegOffsetPair = 0xBFC0BFC0u;  // -1.5, -1.5
+  __device__ static u32x4_t decode(uint32_t w) { return decode_nibbles(w); }
+  __device__ static f32x4_t mma(u32x4_t a, u32x4_t b, f32x4_t c) { return mfma16(a, b, c); }
+  __device__ static uint32_t round(float f) { return f32_to_bf16_rne(f); }
+  __device__ static float widen(uint32_t h) { return bf16_lo(h); }
+};
+
+// fp16: 1.0 = 0x3C00, 10 mantissa bits, so q/16 sits at bit 6 and the
+// biased nibble (q + 8 = nibble ^ 8) lands in bits 6..9: 0x3C00 | 0x0200
+// is 1.5, and nibble k moves to bit 6 of its half with one shift.
+struct ActF16 {
+  static constexpr uint32_t kNegOffsetPair = 0xBE00BE00u;  // -1.5, -1.5
+  __device__ static u32x4_t decode(uint32_t w) {
+    u32x4_t a;
+    a[0] = ((w << 6) & 0x03C003C0u) ^ 0x3E003E00u;
+    a[1] = ((w << 2) & 0x03C003C0u) ^ 0x3E003E00u;
+    a[2] = ((w >> 2) & 0x03C003C0u) ^ 0x3E003E00u;
+    a[3] = ((w >> 6) & 0x03C003C0u) ^ 0x3E003E00u;
+    return a;
+  }
+  __device__ static f32x4_t mma(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  // round to nearest even (v_cvt_f16_f32 under the default rounding mode)
+  __device__ static uint32_t round(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+  __device__ static float widen(uint32_t h) { return half_bits_to_f32(h & 0xFFFFu); }
+};
+
+// -1.5 * (sum over the group of this lane-set's activation rows) in the
+// activation type Act.
+template <class Act>
+__device__ __forceinline__ f32x4_t group_offset_t(const u32x4_t (&xa)[4]) {
+  const u32x4_t neg = {Act::kNegOffsetPair, Act::kNegOffsetPair, Act::kNegOffsetPair,
+                       Act::kNegOffsetPair};
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t c = Act::mma(xa[0], neg, zero);
+  c = Act::mma(xa[1], neg, c);
+  c = Act::mma(xa[2], neg, c);
+  c = Act::mma(xa[3], neg, c);
+  return c;
+}
+
 __device__ __forceinline__ void load_group_x(u32x4_t (&xa)[4], const u32x4_t* xgroup, int a) {
 #pragma unroll
   for (int d = 0; d < 4; ++d) xa[d] = xgroup[4 * a + d];
@@ -222,7 +271,7 @@ __device__ __forceinline__ void stream_load_t(StreamUnit& u, const ProjTable& P,
 // One group of one 16-row weight tile against CT 16-row activation tiles:
 // the offset chain comes from the workgroup's table (corr_g), the weight
 // chain seeds from it, and the epilogue applies this lane's row scale.
-template <int NR, int CT>
+template <int NR, int CT, class Act = ActBf16>
 __device__ __forceinline__ void stream_group(f32x4_t (&acc)[CT], const u32x4_t* const (&xrow)[CT],
                                              int g, u32x4_t w, const float* corr_g, float s,
                                              int a) {
@@ -239,9 +288,9 @@ __device__ __forceinline__ void stream_group(f32x4_t (&acc)[CT], const u32x4_t* 
   }
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    const u32x4_t B = decode_nibbles(w[d]);
+    const u32x4_t B = Act::decode(w[d]);
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) t[ct] = mfma16(xa[ct][d], B, t[ct]);
+    for (int ct = 0; ct < CT; ++ct) t[ct] = Act::mma(xa[ct][d], B, t[ct]);
   }
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct)
@@ -256,7 +305,7 @@ __device__ __forceinline__ void stream_group(f32x4_t (&acc)[CT], const u32x4_t* 
 // so it produces the same bits as the kernels that walk units serially.
 
 // One unit (up to 8 groups) of one weight tile into `part`.
-template <int NR, int CT>
+template <int NR, int CT, class Act = ActBf16>
 __device__ __forceinline__ void stream_unit(f32x4_t (&part)[CT], const StreamUnit& cu,
                                             const u32x4_t* const (&xrow)[CT], const float* corr,
                                             int g0, int gn, int a) {
@@ -264,18 +313,18 @@ __device__ __forceinline__ void stream_unit(f32x4_t (&part)[CT], const StreamUni
     // full unit: straight-line, so independent group chains interleave
 #pragma unroll
     for (int gg = 0; gg < kUnit; ++gg)
-      stream_group<NR, CT>(part, xrow, g0 + gg, cu.w[gg], corr + (g0 + gg) * 16 * CT,
-                           unit_scale(cu.s, gg), a);
+      stream_group<NR, CT, Act>(part, xrow, g0 + gg, cu.w[gg], corr + (g0 + gg) * 16 * CT,
+                                unit_scale(cu.s, gg), a);
   } else {
 #pragma unroll
     for (int gg = 0; gg < kUnit; ++gg)
       if (gg < gn)
-        stream_group<NR, CT>(part, xrow, g0 + gg, cu.w[gg], corr + (g0 + gg) * 16 * CT,
-                             unit_scale(cu.s, gg), a);
+        stream_group<NR, CT, Act>(part, xrow, g0 + gg, cu.w[gg], corr + (g0 + gg) * 16 * CT,
+                                  unit_scale(cu.s, gg), a);
   }
 }
 
-template <int NR, int CT>
+template <int NR, int CT, class Act = ActBf16>
 __device__ __forceinline__ void store_tile(const ProjTable& P, int t, const f32x4_t (&total)[CT],
                                            int M, int i, int a) {
   const int j = proj_of(P, t);
@@ -289,7 +338,7 @@ __device__ __forceinline__ void store_tile(const ProjTable& P, int t, const f32x
       const int m = ct * 16 + 4 * a + r;
       if (m < M && n < Nj)
         Yj[static_cast<size_t>(m) * Nj + n] =
-            static_cast<uint16_t>(f32_to_bf16_rne(16.0f * total[ct][r]));
+            static_cast<uint16_t>(Act::round(16.0f * total[ct][r]));
     }
 }
 
@@ -297,7 +346,7 @@ __device__ __forceinline__ void store_tile(const ProjTable& P, int t, const f32x
 // order), then the -1.5 * sum_k x table per (group, row), which is the same
 // for every weight tile (waves split the groups). Returns the LDS offset
 // table; xrow[ct] is this lane's activation row of column tile ct.
-template <int CT>
+template <int CT, class Act = ActBf16>
 __device__ __forceinline__ float* stream_prologue(u32x4_t* xs, const u32x4_t* (&xrow)[CT],
                                                   const uint16_t* __restrict__ X, int K, int M,
                                                   int wave, int i, int a) {
@@ -313,7 +362,7 @@ __device__ __forceinline__ float* stream_prologue(u32x4_t* xs, const u32x4_t* (&
     for (int ct = 0; ct < CT; ++ct) {
       u32x4_t xa[4];
       load_group_x(xa, xrow[ct] + g * 16, a);
-      const f32x4_t c = group_offset(xa);
+      const f32x4_t c = group_offset_t<Act>(xa);
       if (i == 0) *reinterpret_cast<f32x4_t*>(corr + (g * CT + ct) * 16 + 4 * a) = c;
     }
   }
@@ -326,7 +375,7 @@ __device__ __forceinline__ float* stream_prologue(u32x4_t* xs, const u32x4_t* (&
 // up to 8 groups, prefetching the next unit while the current one is
 // multiplied. NR = accumulator rows per lane that can hold outputs (1 when
 // M == 1, else 4).
-template <bool PACKED, int NR, bool SVEC, int CT>
+template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
     const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
   extern __shared__ u32x4_t xs[];
@@ -344,7 +393,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
   StreamUnit cur, nxt;
   stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t, ntiles - 1), 0, lane);
   const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT>(xs, xrow, X, K, M, wave, i, a);
+  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a);
   if (!active) return;
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -364,14 +413,14 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
     stream_load_t<PACKED, SVEC>(nxt, P, K, G, has_next ? nt : t, has_next ? nu * kUnit : u * kUnit,
                                 lane);
     const int g0 = u * kUnit;
-    stream_unit<NR, CT>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
+    stream_unit<NR, CT, Act>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       total[ct] = total[ct] + part[ct];
       part[ct] = zero;
     }
     if (u == U - 1) {
-      store_tile<NR, CT>(P, t, total, M, i, a);
+      store_tile<NR, CT, Act>(P, t, total, M, i, a);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
     }
@@ -387,7 +436,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
 // partials of those tiles side by side, park them in LDS, and the unit
 // partials of each tile are summed in unit order. Same bits as the stream
 // kernel; shorter latency when tiles alone cannot fill the machine.
-template <bool PACKED, int NR, bool SVEC, int CT>
+template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
     const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
   extern __shared__ u32x4_t xs[];
@@ -412,7 +461,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
     stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t0 + sl / U, ntiles - 1), (sl % U) * kUnit, lane);
   }
   const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT>(xs, xrow, X, K, M, wave, i, a);
+  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a);
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int sl = wave; sl < nslots; sl += kStreamWaves) {
@@ -423,7 +472,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
     const int g0 = (sl % U) * kUnit;
-    stream_unit<NR, CT>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
+    stream_unit<NR, CT, Act>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) slots[(sl * CT + ct) * 64 + lane] = part[ct];
   }
@@ -435,7 +484,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
       total[ct] = zero;
       for (int u = 0; u < U; ++u) total[ct] = total[ct] + slots[((wave * U + u) * CT + ct) * 64 + lane];
     }
-    store_tile<NR, CT>(P, t0 + wave, total, M, i, a);
+    store_tile<NR, CT, Act>(P, t0 + wave, total, M, i, a);
   }
 }
 
@@ -868,6 +917,7 @@ __device__ __forceinline__ uint32_t load_u16_bytes(const uint8_t* p) {
   return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8);
 }
 
+template <class Act>
 __global__ __launch_bounds__(256) void w4a16_bytewise_kernel(
     const uint8_t* __restrict__ W, const uint8_t* __restrict__ Sb,
     const uint8_t* __restrict__ Xb, uint8_t* __restrict__ Yb, int N, int K) {
@@ -885,15 +935,15 @@ __global__ __launch_bounds__(256) void w4a16_bytewise_kernel(
     const float s = half_bits_to_f32(load_u16_bytes(srow + 2 * (b >> 6)));
     const int lo = static_cast<int>(static_cast<int8_t>(static_cast<uint8_t>(byte << 4))) >> 4;
     const int hi = static_cast<int>(static_cast<int8_t>(static_cast<uint8_t>(byte))) >> 4;
-    const float x0 = bf16_lo(load_u16_bytes(xrow + 4 * b));
-    const float x1 = bf16_lo(load_u16_bytes(xrow + 4 * b + 2));
+    const float x0 = Act::widen(load_u16_bytes(xrow + 4 * b));
+    const float x1 = Act::widen(load_u16_bytes(xrow + 4 * b + 2));
     acc += (static_cast<float>(lo) * s) * x0;
     acc += (static_cast<float>(hi) * s) * x1;
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
   if (lane == 0) {
-    const uint32_t y = f32_to_bf16_rne(acc);
+    const uint32_t y = Act::round(acc);
     uint8_t* yp = Yb + (static_cast<size_t>(m) * N + row) * 2;
     yp[0] = static_cast<uint8_t>(y & 0xFF);
     yp[1] = static_cast<uint8_t>(y >> 8);
@@ -1024,7 +1074,7 @@ int stream_occupancy() {
   return occ;
 }
 
-template <bool PACKED, int NR, bool SVEC, int CT>
+template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   const size_t lds = stream_lds_bytes(K, M);
   const int ntiles = P.tile_end[P.count - 1];
@@ -1034,19 +1084,19 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   if (lds_fit < per_cu) per_cu = lds_fit > 0 ? lds_fit : 1;
   const int cap = cu_count() * per_cu;
   const int grid = want < cap ? want : cap;
-  auto kern = w4a16_stream_kernel<PACKED, NR, SVEC, CT>;
+  auto kern = w4a16_stream_kernel<PACKED, NR, SVEC, CT, Act>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kStreamWaves * 64), lds, stream, P, X, K, M);
   return launch_status();
 }
 
-template <bool PACKED, int NR, bool SVEC, int CT>
+template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   const size_t lds = split_lds_bytes(K, M);
   const int ntiles = P.tile_end[P.count - 1];
   const int tpr = split_tiles_per_round(K);
   const int grid = (ntiles + tpr - 1) / tpr;
-  auto kern = w4a16_split_kernel<PACKED, NR, SVEC, CT>;
+  auto kern = w4a16_split_kernel<PACKED, NR, SVEC, CT, Act>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kStreamWaves * 64), lds, stream, P, X, K, M);
   return launch_status();
@@ -1104,7 +1154,7 @@ bool prefer_split(const ProjTable& P, int K, int M) {
   return U >= 2 && split_fits(K, M) && P.tile_end[P.count - 1] < 2 * cu_count();
 }
 
-template <bool PACKED, bool SPLIT>
+template <bool PACKED, bool SPLIT, class Act = ActBf16>
 int launch_stream_any(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   const int G = K / kGroup;
   bool svec = false;
@@ -1113,18 +1163,18 @@ int launch_stream_any(const ProjTable& P, const uint16_t* X, int K, int M, hipSt
     for (int j = 0; j < P.count; ++j) svec = svec && aligned(P.s[j], 16);
   }
 #define W4A16_LAUNCH(NR, SV, CT)                                          \
-  (SPLIT ? launch_split_t<PACKED, NR, SV, CT>(P, X, K, M, stream)         \
-         : launch_stream_t<PACKED, NR, SV, CT>(P, X, K, M, stream))
+  (SPLIT ? launch_split_t<PACKED, NR, SV, CT, Act>(P, X, K, M, stream)    \
+         : launch_stream_t<PACKED, NR, SV, CT, Act>(P, X, K, M, stream))
   if (M > 16) return svec ? W4A16_LAUNCH(4, true, 2) : W4A16_LAUNCH(4, false, 2);
   if (M == 1) return svec ? W4A16_LAUNCH(1, true, 1) : W4A16_LAUNCH(1, false, 1);
   return svec ? W4A16_LAUNCH(4, true, 1) : W4A16_LAUNCH(4, false, 1);
 #undef W4A16_LAUNCH
 }
 
-template <bool PACKED>
+template <bool PACKED, class Act = ActBf16>
 int launch_stream(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
-  return prefer_split(P, K, M) ? launch_stream_any<PACKED, true>(P, X, K, M, stream)
-                               : launch_stream_any<PACKED, false>(P, X, K, M, stream);
+  return prefer_split(P, K, M) ? launch_stream_any<PACKED, true, Act>(P, X, K, M, stream)
+                               : launch_stream_any<PACKED, false, Act>(P, X, K, M, stream);
 }
 
 ProjTable single_table(const uint8_t* W, const uint16_t* S, uint16_t* Y, int N) {
@@ -1200,10 +1250,11 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
   }
 }
 
+template <class Act = ActBf16>
 int launch_bytewise(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                     int K, int M, hipStream_t stream) {
   if (M > 65535) return CUDALM_W4A16_ERANGE;
-  hipLaunchKernelGGL(w4a16_bytewise_kernel, dim3((N + 3) / 4, M), dim3(256), 0, stream, W,
+  hipLaunchKernelGGL(w4a16_bytewise_kernel<Act>, dim3((N + 3) / 4, M), dim3(256), 0, stream, W,
                      reinterpret_cast<const uint8_t*>(S), reinterpret_cast<const uint8_t*>(X),
                      reinterpret_cast<uint8_t*>(Y), N, K);
   return launch_status();
@@ -1252,6 +1303,25 @@ int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y
     default:
       return CUDALM_W4A16_EVARIANT;
   }
+}
+
+// fp16-activation twin: M rows in chunks that fit the stream kernels' LDS
+// (one launch when M <= 32 and x fits), the byte-wise kernel for
+// misaligned file-layout bases.
+template <bool PACKED>
+int f16_dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
+                 int K, int M, bool vec_ok, hipStream_t stream) {
+  if (!vec_ok) return launch_bytewise<ActF16>(W, S, X, Y, N, K, M, stream);
+  int mc = M < 32 ? M : 32;
+  while (mc > 0 && !stream_fits(K, mc)) --mc;
+  if (mc < 1) return CUDALM_W4A16_ERANGE;
+  for (int m0 = 0; m0 < M; m0 += mc) {
+    const int rows = M - m0 < mc ? M - m0 : mc;
+    const ProjTable P = single_table(W, S, Y + static_cast<size_t>(m0) * N, N);
+    if (int rc = launch_stream<PACKED, ActF16>(P, X + static_cast<size_t>(m0) * K, K, rows, stream))
+      return rc;
+  }
+  return CUDALM_W4A16_OK;
 }
 
 }  // namespace
@@ -1377,6 +1447,23 @@ int cudalm_w4a16_gemv_bf16_multi(const cudalm_w4a16_proj* projs, int count, cons
   return prepacked ? launch_stream<true>(P, x, K, M, stream) : launch_stream<false>(P, x, K, M, stream);
 }
 
+int cudalm_w4a16_gemv_f16(const uint8_t* weight, const uint16_t* scale, const uint16_t* x,
+                          uint16_t* y, int N, int K, int M, hipStream_t stream) {
+  if (int rc = check_shape(N, K, M)) return rc;
+  if (!weight || !scale || !x || !y) return CUDALM_W4A16_ENULL;
+  const bool vec_ok = aligned(weight, 16) && aligned(x, 16) && aligned(scale, 2) && aligned(y, 2);
+  return f16_dispatch<false>(weight, scale, x, y, N, K, M, vec_ok, stream);
+}
+
+int cudalm_w4a16_gemv_f16_prepacked(const void* packed, const uint16_t* x, uint16_t* y, int N,
+                                    int K, int M, hipStream_t stream) {
+  if (int rc = check_shape(N, K, M)) return rc;
+  if (!packed || !x || !y) return CUDALM_W4A16_ENULL;
+  if (!aligned(packed, 16) || !aligned(x, 16) || !aligned(y, 2)) return CUDALM_W4A16_EALIGN;
+  return f16_dispatch<true>(static_cast<const uint8_t*>(packed), nullptr, x, y, N, K, M, true,
+                            stream);
+}
+
 int cudalm_silu_mul_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* y, size_t n,
                          hipStream_t stream) {
   if (n == 0) return CUDALM_W4A16_OK;
@@ -1440,7 +1527,7 @@ int cudalm_w4a16_kernel_regs(int variant) {
     case CUDALM_W4A16_VARIANT_TILE16: return regs_of(w4a16_tile_kernel<1, 1, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_TILE32: return regs_of(w4a16_tile_kernel<1, 2, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_gemm_kernel<2, 2, 2, 2, 2, true>);
-    case CUDALM_W4A16_VARIANT_BYTEWISE: return regs_of(w4a16_bytewise_kernel);
+    case CUDALM_W4A16_VARIANT_BYTEWISE: return regs_of(w4a16_bytewise_kernel<ActBf16>);
     case CUDALM_W4A16_VARIANT_SPLIT: return regs_of(w4a16_split_kernel<true, 1, false, 1>);
     case CUDALM_W4A16_VARIANT_SWIGLU: return regs_of(w4a16_swiglu_kernel<true, 1, false, 1>);
     default: return -1;

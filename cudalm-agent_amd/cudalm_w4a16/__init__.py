@@ -48,6 +48,8 @@ _SIGS = {
     "cudalm_w4a16_dequant_f32": ([_P, _P, _P, _P, _I, _I, _P], _I),
     "cudalm_w4a16_gemv_bf16_multi": ([_P, _I, _P, _I, _I, _I, _P], _I),
     "cudalm_w4a16_kernel_regs": ([_I], _I),
+    "cudalm_w4a16_gemv_f16": ([_P, _P, _P, _P, _I, _I, _I, _P], _I),
+    "cudalm_w4a16_gemv_f16_prepacked": ([_P, _P, _P, _I, _I, _I, _P], _I),
     "cudalm_w4a16_swiglu_bf16": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P], _I),
     "cudalm_silu_mul_bf16": ([_P, _P, _P, _SZ, _P], _I),
     "cudalm_bf16_gemv": ([_P, _P, _P, _I, _I, _I, _P], _I),
@@ -287,6 +289,38 @@ def gemv_multi(weights, scales, x, Ns, K: int, M: int = 1, ys=None, prepacked: b
                                            K, M, int(prepacked), _stream(stream))
     _check(rc, "cudalm_w4a16_gemv_bf16_multi")
     return ys
+
+
+# ---------------------------------------------------------------------------
+# fp16-activation twin (int4_gemv)
+# ---------------------------------------------------------------------------
+
+def gemv_f16(weight, scale, x, N: int, K: int, M: int = 1, y=None, stream=None):
+    """y[M, N] fp16 = W4A16(weight, scale) @ x[M, K] fp16."""
+    import torch
+
+    if y is None:
+        y = torch.empty((M, N) if M > 1 else (N,), dtype=torch.float16, device=x.device)
+    rc = _lib.cudalm_w4a16_gemv_f16(_ptr(weight), _ptr(scale), _ptr(x), _ptr(y), N, K, M,
+                                    _stream(stream))
+    _check(rc, "cudalm_w4a16_gemv_f16")
+    return y
+
+
+def gemv_f16_prepacked(packed, x, N: int, K: int, M: int = 1, y=None, stream=None):
+    import torch
+
+    if y is None:
+        y = torch.empty((M, N) if M > 1 else (N,), dtype=torch.float16, device=x.device)
+    rc = _lib.cudalm_w4a16_gemv_f16_prepacked(_ptr(packed), _ptr(x), _ptr(y), N, K, M,
+                                              _stream(stream))
+    _check(rc, "cudalm_w4a16_gemv_f16_prepacked")
+    return y
+
+
+def int4_gemv(weight, scales, x, y, N: int, K: int, stream=None):
+    """Reference name and argument order (int4_gemv.h:39-40)."""
+    return gemv_f16(weight, scales, x, N, K, 1, y=y, stream=stream)
 
 
 # ---------------------------------------------------------------------------

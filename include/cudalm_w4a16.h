@@ -112,6 +112,21 @@ int cudalm_w4a16_gemv_bf16_multi(const cudalm_w4a16_proj* projs, int count,
                                  const uint16_t* x, int K, int M, int prepacked,
                                  hipStream_t stream);
 
+/* fp16-activation twin of cudalm_w4a16_gemv_bf16: x and y are fp16 bit
+ * patterns, y[m, n] = fp16_rne( sum_k q * f32(scale) * f32(x[m, k]) ) with
+ * fp32 accumulation. Replaces int4_gemv (M == 1; include/cudalm/kernels/
+ * int4_gemv.h:22-40); any M (chunks of up to 32 rows), row m bit-identical
+ * to the M == 1 call. Misaligned weight / x bases take a byte-wise kernel. */
+int cudalm_w4a16_gemv_f16(const uint8_t* weight, const uint16_t* scale,
+                          const uint16_t* x, uint16_t* y, int N, int K, int M,
+                          hipStream_t stream);
+
+/* Same from the prepacked layout (packed and x 16 B aligned, else EALIGN);
+ * bit-identical to cudalm_w4a16_gemv_f16 on the file layout. */
+int cudalm_w4a16_gemv_f16_prepacked(const void* packed, const uint16_t* x,
+                                    uint16_t* y, int N, int K, int M,
+                                    hipStream_t stream);
+
 /* SwiGLU MLP front half in one launch: the gate and up projections of the
  * same x[M, K] (both [N, K], file layout with scales or both prepacked)
  * and the epilogue

@@ -53,6 +53,9 @@ _SIGS = {
     "orc_hardware_threads": ([], ctypes.c_int),
     "orc_silu_bf16": ([ctypes.c_uint16], ctypes.c_uint16),
     "orc_silu_mul_bf16": ([_P, _P, _P, ctypes.c_size_t], None),
+    "orc_gemv_f16": ([_P, _P, _P, _P, _I64, _I64, _I64], None),
+    "orc_gemv_f16_f64": ([_P, _P, _P, _P, _P, _I64, _I64, _I64], None),
+    "orc_fixture_gemv_f16": ([ctypes.c_uint32, _I64, _I64, _P, _P, _P], None),
     "orc_bf16_fixture": ([ctypes.c_uint32, _I64, _I64, _P, _P], None),
     "orc_bf16_gemv": ([_P, _P, _P, _I64, _I64, _I64], None),
     "orc_bf16_gemv_mt": ([_P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
@@ -244,6 +247,55 @@ def check_tolerance(y_bits, W, S, X, N, K, M, ulps: float = 2.0):
     return check_tolerance_f64(y_bits, r, a, M, N, ulps)
 
 
+# ---- fp16-activation twin (int4_gemv) ----------------------------------------
+
+def fixture_gemv_f16(seed: int, N: int, K: int):
+    """test_int4_gemv.cpp:70-83: (W u8, S fp16 bits, x fp16 bits [1, K])."""
+    W = np.empty((N, K // 2), np.uint8)
+    S = np.empty((N, K // 128), np.uint16)
+    X = np.empty((1, K), np.uint16)
+    _lib.orc_fixture_gemv_f16(seed, N, K, _p(W), _p(S), _p(X))
+    return W, S, X
+
+
+def gemv_f16(W, S, X, N: int, K: int, M: int = 1) -> np.ndarray:
+    """ref_gemv of test_int4_gemv.cpp:49-63, M rows: fp16 bits [M, N]."""
+    Y = np.empty((M, N), np.uint16)
+    _lib.orc_gemv_f16(_p(W), _p(S), _p(X), _p(Y), N, K, M)
+    return Y
+
+
+def gemv_f16_f64(W, S, X, N: int, K: int, M: int = 1):
+    Y = np.empty((M, N), np.float64)
+    A = np.empty((M, N), np.float64)
+    _lib.orc_gemv_f16_f64(_p(W), _p(S), _p(X), _p(Y), _p(A), N, K, M)
+    return Y, A
+
+
+def fp16_ulp(v: np.ndarray) -> np.ndarray:
+    """Spacing of fp16 numbers at |v| (subnormal spacing 2^-24 below 2^-14)."""
+    a = np.abs(np.asarray(v, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def check_f16_tolerance(y_bits, W, S, X, N, K, M, ulps: float = 2.0):
+    """|y - r| <= ulps * ulp_fp16(r) + CANCEL_FLOOR * sum|terms| for finite
+    r within the fp16 range; outputs whose exact value overflows fp16 must
+    be infinities of the right sign."""
+    r, a = gemv_f16_f64(W, S, X, N, K, M)
+    y = fp16_to_f32(np.asarray(y_bits, np.uint16).reshape(M, N)).astype(np.float64)
+    big = np.abs(r) >= 65520.0  # rounds to +-inf in fp16
+    err = np.abs(y - r)
+    tol = ulps * fp16_ulp(r) + CANCEL_FLOOR * a
+    bad = ~(err <= tol) & ~big
+    bad |= big & ~(np.isinf(y) & (np.sign(y) == np.sign(r)))
+    ulp_dist = np.where(big, 0.0, err / fp16_ulp(r))
+    stats = {"max_ulp": float(ulp_dist.max()) if err.size else 0.0, "n_bad": int(bad.sum()),
+             "n_over_2ulp": int((ulp_dist > 2.0).sum()), "n": int(err.size)}
+    return not bad.any(), stats
+
+
 # ---- SwiGLU element-wise stage ---------------------------------------------
 
 def silu_bf16(g_bits) -> np.ndarray:
@@ -330,6 +382,8 @@ class _Ref:
         self.lib.ref_compare_bf16_stages.argtypes = [_P, _P, ctypes.c_size_t, ctypes.c_double,
                                                      ctypes.c_double, _P, _P]
         self.lib.ref_compare_bf16_stages.restype = ctypes.c_int
+        self.lib.ref_compare_fp16_stages.argtypes = self.lib.ref_compare_bf16_stages.argtypes
+        self.lib.ref_compare_fp16_stages.restype = ctypes.c_int
 
     def fp16_to_f32(self, h: int) -> float:
         return self.lib.ref_fp16_bits_to_f32(h)
@@ -343,6 +397,16 @@ class _Ref:
         mx = ctypes.c_double()
         idx = ctypes.c_size_t()
         ok = self.lib.ref_compare_bf16_stages(_p(r), _p(a), r.size, atol, rtol, ctypes.byref(mx),
+                                              ctypes.byref(idx))
+        return bool(ok), mx.value, idx.value
+
+
+    def compare_fp16_stages(self, ref_bits, act_bits, atol=1e-2, rtol=1e-2):
+        r = np.ascontiguousarray(ref_bits, np.uint16).ravel()
+        a = np.ascontiguousarray(act_bits, np.uint16).ravel()
+        mx = ctypes.c_double()
+        idx = ctypes.c_size_t()
+        ok = self.lib.ref_compare_fp16_stages(_p(r), _p(a), r.size, atol, rtol, ctypes.byref(mx),
                                               ctypes.byref(idx))
         return bool(ok), mx.value, idx.value
 

@@ -30,4 +30,14 @@ int ref_compare_bf16_stages(const std::uint16_t* ref, const std::uint16_t* act, 
   return r.ok ? 1 : 0;
 }
 
+// Returns 1 when every element passes |a - r| <= atol + rtol * |r| (fp16).
+int ref_compare_fp16_stages(const std::uint16_t* ref, const std::uint16_t* act, std::size_t n,
+                            double atol, double rtol, double* max_abs_err,
+                            std::size_t* max_abs_idx) {
+  const cudalm::StageCompareResult r = cudalm::compare_fp16_stages(ref, act, n, atol, rtol);
+  if (max_abs_err) *max_abs_err = r.max_abs_err;
+  if (max_abs_idx) *max_abs_idx = r.max_abs_idx;
+  return r.ok ? 1 : 0;
+}
+
 }

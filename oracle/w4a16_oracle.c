@@ -275,6 +275,51 @@ void orc_gemv_bf16_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X,
   for (int t = 0; t < used; ++t) pthread_join(th[t], NULL);
 }
 
+/* ref_gemv of tests/cuda/test_int4_gemv.cpp:49-63 (fp16 activations and
+ * output): per output a sequential fp32 loop over bytes b, adding
+ * (lo * s) * x[2b] then (hi * s) * x[2b+1], one fp16 RNE at the end. */
+void orc_gemv_f16(const uint8_t* W, const uint16_t* S, const uint16_t* X,
+                  uint16_t* Y, int64_t N, int64_t K, int64_t M) {
+  const int64_t G = K / 128;
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      const uint8_t* wrow = W + n * (K / 2);
+      const uint16_t* srow = S + n * G;
+      float acc = 0.0f;
+      for (int64_t b = 0; b < K / 2; ++b) {
+        const float s = orc_fp16_to_f32(srow[b >> 6]);
+        int lo, hi;
+        orc_unpack_byte(wrow[b], &lo, &hi);
+        acc += (float)lo * s * orc_fp16_to_f32(X[m * K + 2 * b]);
+        acc += (float)hi * s * orc_fp16_to_f32(X[m * K + 2 * b + 1]);
+      }
+      Y[m * N + n] = orc_f32_to_fp16_rne(acc);
+    }
+  }
+}
+
+/* fp64 sum of the exact fp32 terms with fp16 activations, and |terms|. */
+void orc_gemv_f16_f64(const uint8_t* W, const uint16_t* S, const uint16_t* X,
+                      double* Y, double* Yabs, int64_t N, int64_t K, int64_t M) {
+  const int64_t G = K / 128;
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      double acc = 0.0, aacc = 0.0;
+      for (int64_t b = 0; b < K / 2; ++b) {
+        const double s = (double)orc_fp16_to_f32(S[n * G + (b >> 6)]);
+        int lo, hi;
+        orc_unpack_byte(W[n * (K / 2) + b], &lo, &hi);
+        const double t0 = (double)lo * s * (double)orc_fp16_to_f32(X[m * K + 2 * b]);
+        const double t1 = (double)hi * s * (double)orc_fp16_to_f32(X[m * K + 2 * b + 1]);
+        acc += t0 + t1;
+        aacc += fabs(t0) + fabs(t1);
+      }
+      Y[m * N + n] = acc;
+      if (Yabs) Yabs[m * N + n] = aacc;
+    }
+  }
+}
+
 /* fp64 accumulation of the exact fp32 terms (q*s)*x; also returns the sum
  * of |terms| (the scale of the accumulated rounding error). */
 void orc_gemv_f64(const uint8_t* W, const uint16_t* S, const uint16_t* X,
@@ -335,6 +380,16 @@ void orc_fixture_gemv(uint32_t seed, int64_t N, int64_t K, uint8_t* W,
   for (int64_t i = 0; i < N * (K / 2); ++i) W[i] = (uint8_t)orc_xorshift32_next(&s);
   for (int64_t i = 0; i < N * (K / 128); ++i) S[i] = rng_scale(&s);
   for (int64_t i = 0; i < K; ++i) X[i] = orc_f32_to_bf16_rne(rng_n01(&s));
+}
+
+/* tests/cuda/test_int4_gemv.cpp:70-83 (the fp16 twin's fixture): the same
+ * draws as orc_fixture_gemv with x stored as fp16 RNE. */
+void orc_fixture_gemv_f16(uint32_t seed, int64_t N, int64_t K, uint8_t* W,
+                          uint16_t* S, uint16_t* X) {
+  uint32_t s = seed ? seed : 0x9e3779b9u;
+  for (int64_t i = 0; i < N * (K / 2); ++i) W[i] = (uint8_t)orc_xorshift32_next(&s);
+  for (int64_t i = 0; i < N * (K / 128); ++i) S[i] = rng_scale(&s);
+  for (int64_t i = 0; i < K; ++i) X[i] = orc_f32_to_fp16_rne(rng_n01(&s));
 }
 
 /* test_w4a16_qwen35_optimized.cpp:66-135 (make_fixture with InputKind).

@@ -24,6 +24,9 @@
  *                        shapes (bit-exact), fp64 matmul bound at all shapes,
  *                        closed forms (zero row, one-hot x, linearity, sign)
  *   orc_gemv_f64         numpy float64 matmul of the dequantized weights
+ *   orc_gemv_f16         as orc_gemv_bf16, with numpy float16 activations and
+ *                        output (brute force bit-exact, fp64 bound, closed
+ *                        forms); orc_gemv_f16_f64 as orc_gemv_f64
  *   orc_rng_*            xorshift32 known-answer sequence vs a Python restatement
  */
 #ifndef CUDALM_W4A16_ORACLE_H
@@ -66,6 +69,11 @@ void orc_gemv_bf16_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X,
 void orc_gemv_f64(const uint8_t* W, const uint16_t* S, const uint16_t* X,
                   double* Y, double* Yabs, int64_t N, int64_t K, int64_t M);
 
+void orc_gemv_f16(const uint8_t* W, const uint16_t* S, const uint16_t* X,
+                  uint16_t* Y, int64_t N, int64_t K, int64_t M);
+void orc_gemv_f16_f64(const uint8_t* W, const uint16_t* S, const uint16_t* X,
+                      double* Y, double* Yabs, int64_t N, int64_t K, int64_t M);
+
 /* ---- seeded fixtures ---------------------------------------------------- */
 uint32_t orc_xorshift32_next(uint32_t* state);
 void orc_xorshift32_fill(uint32_t seed, uint32_t* out, size_t n);
@@ -78,6 +86,8 @@ enum {
 };
 void orc_fixture_gemv(uint32_t seed, int64_t N, int64_t K, uint8_t* W,
                       uint16_t* S, uint16_t* X);
+void orc_fixture_gemv_f16(uint32_t seed, int64_t N, int64_t K, uint8_t* W,
+                          uint16_t* S, uint16_t* X);
 void orc_fixture_kind(int kind, uint32_t seed, int64_t N, int64_t K,
                       int64_t B, uint8_t* W, uint16_t* S, uint16_t* X);
 void orc_synth_normal_f32(uint64_t seed, float sigma, float* out, size_t n);

@@ -117,6 +117,8 @@ def test_cpp_headers_compile_and_link(tmp_path, w4):
 #include "cudalm/kernels/int4_gemv_bf16.h"
 #include "cudalm/kernels/batch_decode.h"
 #include "cudalm/kernels/bf16_gemv.h"
+#include "cudalm/kernels/int4_gemv.h"
+#include "cudalm/kernels/swiglu.h"
 #include "cudalm/w4a16_linear.h"
 #include "cudalm_bf16_gemv.h"
 #include "cudalm_v2.h"
@@ -129,7 +131,11 @@ int main() {
       cudalm::bf16_gemv;
   void (*f2)(const __hip_bfloat16*, const __hip_bfloat16*, __hip_bfloat16*, int, int, int,
              hipStream_t) = cudalm::kernels::batch_bf16_gemv;
-  return (f1 && f2) ? 0 : 1;
+  void (*f3)(const std::uint8_t*, const __half*, const __half*, __half*, int, int, hipStream_t) =
+      cudalm::int4_gemv;
+  void (*f4)(const __hip_bfloat16*, const __hip_bfloat16*, __hip_bfloat16*, std::size_t,
+             hipStream_t) = cudalm::kernels::qwen35_silu_mul_bf16;
+  return (f1 && f2 && f3 && f4) ? 0 : 1;
 }
 ''')
     exe = tmp_path / "use"
