@@ -15,6 +15,9 @@ Also reported (same JSON line, extra keys):
     head) at M = 1, 8, 32, replayed from a HIP graph: us per decode step,
     and aggregate GB/s;
   * configs[4]: prefill-chunk GEMM, M = 512, per census shape: TFLOP/s;
+  * next_rows: the tied bf16 LM head (M = 1, 8; GB/s), the SwiGLU front
+    half at 3584x1024 (fused launch vs gate -> up -> silu*mul), and the
+    fp16-activation twin on the LM-head workload;
   * cpu_baseline: the oracle's restatement of the reference's CPU path
     (ref_gemv_bf16) on the host cores, LM-head workload.
 
@@ -165,6 +168,31 @@ def graph_time(torch, fn, reps: int, stream):
     return t0.elapsed_time(t1) * 1e-3 / reps
 
 
+def bench_bf16_lm_head(torch, lib, dev, stream, sraw, reps: int = 40):
+    """Tied bf16 LM head (bf16_gemv / batch_bf16_gemv), M = 1 and 8, four
+    rotating 508 MB weight copies; per-launch event timing."""
+    Nb, Kb = LM_HEAD
+    embs = []
+    for c in range(4):
+        g = torch.Generator(device=dev)
+        g.manual_seed(0xE4B + c)
+        embs.append((torch.randn((Nb, Kb), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+    bf = {}
+    for Mb in (1, 8):
+        xb = synth_act(torch, Mb, Kb, 0xB16 + Mb, dev)
+        yb = torch.empty((Mb, Nb), dtype=torch.bfloat16, device=dev)
+        xbp, ybp = xb.data_ptr(), yb.data_ptr()
+        L = [(lambda ep=e.data_ptr(): lib.cudalm_bf16_gemv(ep, xbp, ybp, Nb, Kb, Mb, sraw))
+             for e in embs]
+        per, _ = time_launches(torch, L, reps, 8, stream)
+        byts = 2 * Nb * Kb + 2 * Mb * Kb + 2 * Mb * Nb
+        bf[f"M{Mb}"] = {"kernel_us": round(per * 1e6, 2), "GBps": round(byts / per / 1e9, 1),
+                        "frac_hbm_peak": round(byts / per / 1e9 / HBM_PEAK_GBS, 4),
+                        "algorithmic_bytes": byts}
+    del embs
+    return bf
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -174,14 +202,18 @@ def main():
     ap.add_argument("--no-census", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-next", action="store_true",
+                    help="skip the bf16 LM head, SwiGLU and fp16-twin lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--lm-head-only", action="store_true",
                     help="headline workload only (for counter collection)")
+    ap.add_argument("--bf16-lm-head-only", action="store_true",
+                    help="only the tied bf16 LM head lines (for counter collection)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (x5), to scale HBM counters")
     args = ap.parse_args()
     if args.lm_head_only:
-        args.no_census = args.no_prefill = args.no_cpu = True
+        args.no_census = args.no_prefill = args.no_cpu = args.no_next = True
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the W4A16 projection path runs on a single "
@@ -210,6 +242,11 @@ def main():
     sraw = stream.cuda_stream
     lib = w4.lib()
 
+    if args.bf16_lm_head_only:
+        print(json.dumps({"bf16_lm_head": bench_bf16_lm_head(torch, lib, dev, stream, sraw,
+                                                             reps=args.steps)}), flush=True)
+        return
+
     # ---------------- headline: LM head, M = 1, prepacked ----------------
     N, K = LM_HEAD
     M = 1
@@ -236,15 +273,20 @@ def main():
     launches = [mk_packed(p) for p in packs]
     per_launch, _ = time_launches(torch, launches, min(args.steps, 100), args.warmup, stream)
     torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
     t_start = time.perf_counter()
+    ev0.record(stream)  # HIP events on the stream the kernels run on
     for i in range(args.steps):
         launches[i % len(launches)]()
+    ev1.record(stream)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
     step_s = elapsed / args.steps
+    kern_s = ev0.elapsed_time(ev1) * 1e-3 / args.steps  # back-to-back launches
     nbytes = algo_bytes(N, K, M)
     value = nbytes / step_s / 1e9
-    kern_gbs = nbytes / per_launch / 1e9
+    kern_gbs = nbytes / kern_s / 1e9
 
     file_per = float("nan")
     if not args.lm_head_only:
@@ -334,6 +376,51 @@ def main():
                                  "frac_bf16_peak": round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 4)}
         extra["prefill_M512"] = pre
 
+    # ---------------- next rows: bf16 LM head, SwiGLU epilogue, fp16 twin ----------------
+    if not args.no_next:
+        nxt = {}
+        nxt["bf16_lm_head"] = bench_bf16_lm_head(torch, lib, dev, stream, sraw)
+        # SwiGLU front half at the MLP shape: gate, up, silu*mul
+        Ng, Kg = 3584, 1024
+        gu = []
+        for c in range(16):
+            w, s = synth_weights(torch, Ng, Kg, 0x5C0 + c, dev)
+            gu.append(w4.repack(w, s, Ng, Kg))
+        sw = {}
+        for Mg in (1, 8, 32):
+            xg = synth_act(torch, Mg, Kg, 0x5C1 + Mg, dev)
+            tg = torch.empty((Mg, Ng), dtype=torch.bfloat16, device=dev)
+            tu, yg = torch.empty_like(tg), torch.empty_like(tg)
+            xgp, tgp, tup, ygp = xg.data_ptr(), tg.data_ptr(), tu.data_ptr(), yg.data_ptr()
+            pairs = [(gu[2 * c].data_ptr(), gu[2 * c + 1].data_ptr()) for c in range(8)]
+
+            def three(pairs=pairs, Mg=Mg):
+                for a, b in pairs:
+                    lib.cudalm_w4a16_gemv_bf16_prepacked(a, xgp, tgp, Ng, Kg, Mg, sraw)
+                    lib.cudalm_w4a16_gemv_bf16_prepacked(b, xgp, tup, Ng, Kg, Mg, sraw)
+                    lib.cudalm_silu_mul_bf16(tgp, tup, ygp, Mg * Ng, sraw)
+
+            def one(pairs=pairs, Mg=Mg):
+                for a, b in pairs:
+                    lib.cudalm_w4a16_swiglu_bf16(a, None, b, None, xgp, ygp, Ng, Kg, Mg, 1, sraw)
+
+            t3 = graph_time(torch, three, 10, stream) / len(pairs)
+            t1 = graph_time(torch, one, 10, stream) / len(pairs)
+            sw[f"M{Mg}"] = {"three_launch_us": round(t3 * 1e6, 2), "fused_us": round(t1 * 1e6, 2),
+                            "fused_GBps": round(2 * algo_bytes(Ng, Kg, Mg) / t1 / 1e9, 1)}
+        nxt["swiglu_gate_up_3584x1024"] = sw
+        del gu
+        # fp16-activation twin (int4_gemv) on the LM-head workload
+        xh16 = torch.randn((1, K), device=dev).to(torch.float16)
+        yh16 = torch.empty((1, N), dtype=torch.float16, device=dev)
+        L = [(lambda pp=p.data_ptr(): lib.cudalm_w4a16_gemv_f16_prepacked(pp, xh16.data_ptr(),
+                                                                          yh16.data_ptr(), N, K, 1,
+                                                                          sraw)) for p in packs]
+        per, _ = time_launches(torch, L, 40, 8, stream)
+        nxt["f16_twin_lm_head_M1"] = {"kernel_us": round(per * 1e6, 2),
+                                      "GBps": round(nbytes / per / 1e9, 1)}
+        extra["next_rows"] = nxt
+
     # ---------------- CPU baseline (oracle restatement of ref_gemv_bf16) ----------------
     cpu = None
     if not args.no_cpu:
@@ -376,8 +463,10 @@ def main():
                      "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
                      "traffic_source": "profiles/w4a16_stream_lm_head_M1.md (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0, copy-calibrated)",
-                     "kernel": "w4a16_stream_kernel<true>",
-                     "kernel_us": round(per_launch * 1e6, 3),
+                     "kernel": "w4a16_stream_kernel<true, 1, false, 1>",
+                     "kernel_us": round(kern_s * 1e6, 3),
+                     "kernel_us_source": "HIP events around the timed K launches / K",
+                     "kernel_us_event_pairs": round(per_launch * 1e6, 3),
                      "algorithmic_bytes_per_launch": nbytes},
         "file_layout_entry": ({"kernel_us": round(file_per * 1e6, 3), "GBps": round(file_gbs, 1)}
                               if file_gbs else None),

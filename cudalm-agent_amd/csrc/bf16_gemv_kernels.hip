@@ -202,9 +202,11 @@ int launch_stream_ct(const uint16_t* W, const uint16_t* X, uint16_t* Y, int N, i
   const int per_cu = static_cast<int>(kLdsMax / lds) < stream_wgs_per_cu()
                          ? static_cast<int>(kLdsMax / lds)
                          : stream_wgs_per_cu();
-  const int need = (ntiles + kWaves - 1) / kWaves;
-  const int cap = cu_count() * (per_cu > 0 ? per_cu : 1);
-  const int gx = need < cap ? need : cap;
+  // balanced rounds: every wave walks the same number of tiles
+  const int cap_waves = cu_count() * (per_cu > 0 ? per_cu : 1) * kWaves;
+  const int rounds = (ntiles + cap_waves - 1) / cap_waves;
+  const int waves = (ntiles + rounds - 1) / rounds;
+  const int gx = (waves + kWaves - 1) / kWaves;
   const int gy = (M + mc - 1) / mc;
   if (gy > 65535) return CUDALM_W4A16_ERANGE;
   hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(kWaves * 64), lds, stream, W, X, Y, N, K, M, mc);

@@ -1078,10 +1078,13 @@ template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   const size_t lds = stream_lds_bytes(K, M);
   const int ntiles = P.tile_end[P.count - 1];
-  const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
   int per_cu = stream_occupancy();
   const int lds_fit = static_cast<int>(kLdsMax / (lds > 0 ? lds : 1));
   if (lds_fit < per_cu) per_cu = lds_fit > 0 ? lds_fit : 1;
+  // Persistent: as many workgroups as stay resident (a tile-count-balanced
+  // grid with fewer waves, or one with more than fit, both measured slower
+  // on the LM head than this one-round-uneven split).
+  const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
   const int cap = cu_count() * per_cu;
   const int grid = want < cap ? want : cap;
   auto kern = w4a16_stream_kernel<PACKED, NR, SVEC, CT, Act>;
