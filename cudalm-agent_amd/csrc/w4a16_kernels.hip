@@ -431,6 +431,142 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
   }
 }
 
+// Piece streaming: the same arithmetic as the stream kernel (the 8-group
+// unit partial, then the unit sum), but weights are fetched and consumed in
+// pieces of HG groups (HG divides 8), so the compute that trails a wave's
+// last load is HG/8 of a unit and the first compute starts after HG groups.
+template <int HG>
+struct StreamPiece {
+  u32x4_t w[HG];
+  uint32_t s[HG / 2];  // fp16 scales of the HG groups for this lane's weight row
+};
+
+// Lane addresses of one tile: its weight bytes and its fp16 scales at group
+// 0. Computed once per tile; the pieces add group offsets to them.
+struct TileAddr {
+  const uint8_t* w;
+  const uint8_t* s;
+};
+
+template <bool PACKED>
+__device__ __forceinline__ TileAddr tile_addr(const ProjTable& P, int K, int G, int t, int lane) {
+  const int j = proj_of(P, t);
+  const int rt = t - proj_begin(P, j);
+  const int i = lane & 15, a = lane >> 4;
+  if constexpr (PACKED) {
+    const uint8_t* tile = P.w[j] + static_cast<size_t>(rt) * packed_tile_bytes(G);
+    return {tile + lane * 16, tile + static_cast<size_t>(G) * 1024 + i * packed_scale_pitch(G)};
+  } else {
+    const int row = min(rt * kTileRows + i, P.n[j] - 1);
+    return {P.w[j] + static_cast<size_t>(row) * (K >> 1) + a * 16,
+            reinterpret_cast<const uint8_t*>(P.s[j] + static_cast<size_t>(row) * G)};
+  }
+}
+
+// FULL: G is a multiple of HG, so no group index needs clamping.
+template <int HG, bool PACKED, bool SVEC, bool FULL>
+__device__ __forceinline__ void stream_load_piece(StreamPiece<HG>& h, TileAddr ad, int G, int g0) {
+  static_assert(HG == 2 || HG == 4, "piece of 2 or 4 groups");
+  constexpr int kStep = PACKED ? 1024 : 64;  // bytes between groups of one lane
+  const uint8_t* wp = ad.w + static_cast<size_t>(g0) * kStep;
+#pragma unroll
+  for (int gg = 0; gg < HG; ++gg) {
+    const int off = FULL ? gg : min(g0 + gg, G - 1) - g0;
+    h.w[gg] = *reinterpret_cast<const u32x4_t*>(wp + off * kStep);
+  }
+  if constexpr (PACKED || SVEC) {
+    // packed scale rows are 16 B aligned; SVEC file rows too (G % 8 == 0)
+    if constexpr (HG == 4) {
+      const uint2 sv = *reinterpret_cast<const uint2*>(ad.s + 2 * g0);
+      h.s[0] = sv.x;
+      h.s[1] = sv.y;
+    } else {
+      h.s[0] = *reinterpret_cast<const uint32_t*>(ad.s + 2 * g0);
+    }
+  } else {
+    const uint16_t* srow = reinterpret_cast<const uint16_t*>(ad.s);
+    uint32_t v[HG];
+#pragma unroll
+    for (int gg = 0; gg < HG; ++gg) v[gg] = srow[min(g0 + gg, G - 1)];
+#pragma unroll
+    for (int q = 0; q < HG / 2; ++q) h.s[q] = v[2 * q] | (v[2 * q + 1] << 16);
+  }
+}
+
+template <int HG, int NR, int CT, class Act, bool FULL>
+__device__ __forceinline__ void stream_piece(f32x4_t (&part)[CT], const StreamPiece<HG>& h,
+                                             const u32x4_t* const (&xrow)[CT], const float* corr,
+                                             int g0, int gn, int a) {
+#pragma unroll
+  for (int gg = 0; gg < HG; ++gg) {
+    if (FULL || gg < gn)
+      stream_group<NR, CT, Act>(part, xrow, g0 + gg, h.w[gg], corr + (g0 + gg) * 16 * CT,
+                                half_bits_to_f32((h.s[gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu), a);
+  }
+}
+
+template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, int HG = 4, bool FULL = true>
+__global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_piece_kernel(
+    const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
+  extern __shared__ u32x4_t xs[];
+  constexpr int PPU = kUnit / HG;  // pieces per 8-group unit
+  const int G = K >> 7;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int i = lane & 15, a = lane >> 4;
+  const int ntiles = P.tile_end[P.count - 1];
+  const int H = (G + HG - 1) / HG;  // pieces per tile
+  const int stride = gridDim.x * kStreamWaves;
+  int t = blockIdx.x * kStreamWaves + wave;
+  const bool active = t < ntiles;
+
+  StreamPiece<HG> cur, nxt;
+  TileAddr acur = tile_addr<PACKED>(P, K, G, min(t, ntiles - 1), lane);
+  stream_load_piece<HG, PACKED, SVEC, FULL>(cur, acur, G, 0);
+  const u32x4_t* xrow[CT];
+  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a);
+  if (!active) return;
+
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t part[CT], total[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) part[ct] = total[ct] = zero;
+  int h = 0;
+  while (true) {
+    int nt = t, nh = h + 1;
+    if (nh == H) {
+      nh = 0;
+      nt = t + stride;
+    }
+    const bool has_next = nt < ntiles;
+    TileAddr anx = acur;
+    if (has_next && nh == 0) anx = tile_addr<PACKED>(P, K, G, nt, lane);
+    // past the last piece, re-read the current one (cache hits) instead of
+    // branching around the loads
+    stream_load_piece<HG, PACKED, SVEC, FULL>(nxt, anx, G, (has_next ? nh : h) * HG);
+    const int g0 = h * HG;
+    stream_piece<HG, NR, CT, Act, FULL>(part, cur, xrow, corr, g0, min(HG, G - g0), a);
+    // an 8-group unit ends after its last piece or at the tile's last piece
+    if ((h % PPU) == PPU - 1 || h == H - 1) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        total[ct] = total[ct] + part[ct];
+        part[ct] = zero;
+      }
+    }
+    if (h == H - 1) {
+      store_tile<NR, CT, Act>(P, t, total, M, i, a);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
+    }
+    if (!has_next) break;
+    cur = nxt;
+    acur = anx;
+    t = nt;
+    h = nh;
+  }
+}
+
 // Split kernel: few weight tiles, several units per tile (K >= 2048). A
 // workgroup takes TPR = max(1, 4/U) tiles; its waves compute the unit
 // partials of those tiles side by side, park them in LDS, and the unit
@@ -1061,6 +1197,18 @@ size_t split_lds_bytes(int K, int M) {
 
 bool split_fits(int K, int M) { return M <= 32 && split_lds_bytes(K, M) <= kLdsMax; }
 
+// Stream-kernel fetch granularity (CUDALM_W4A16_STREAM_PIECE, measurement
+// only): 1 = pieces of 4 groups (default), 2 = pieces of 2 groups, 0 = whole
+// 8-group units. Same bits in every mode.
+int stream_half_enabled() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("CUDALM_W4A16_STREAM_PIECE");
+    v = e ? atoi(e) : 1;
+  }
+  return v;
+}
+
 int stream_occupancy() {
   static int occ = 0;
   if (occ == 0) {
@@ -1087,7 +1235,13 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
   const int cap = cu_count() * per_cu;
   const int grid = want < cap ? want : cap;
-  auto kern = w4a16_stream_kernel<PACKED, NR, SVEC, CT, Act>;
+  const int G = K / kGroup;
+  const int mode = stream_half_enabled();
+  auto kern = mode == 2   ? (G % 2 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, true>
+                                          : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, false>)
+              : mode == 1 ? (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true>
+                                          : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false>)
+                          : w4a16_stream_kernel<PACKED, NR, SVEC, CT, Act>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kStreamWaves * 64), lds, stream, P, X, K, M);
   return launch_status();
@@ -1526,7 +1680,8 @@ int cudalm_w4a16_dequant_f32(const uint8_t* weight, const uint16_t* scale, int8_
 int cudalm_w4a16_kernel_regs(int variant) {
   switch (variant) {
     case CUDALM_W4A16_VARIANT_AUTO:
-    case CUDALM_W4A16_VARIANT_STREAM: return regs_of(w4a16_stream_kernel<true, 1, false, 1>);
+    case CUDALM_W4A16_VARIANT_STREAM:
+      return regs_of(w4a16_stream_piece_kernel<true, 1, false, 1, ActBf16, 4, true>);
     case CUDALM_W4A16_VARIANT_TILE16: return regs_of(w4a16_tile_kernel<1, 1, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_TILE32: return regs_of(w4a16_tile_kernel<1, 2, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_gemm_kernel<2, 2, 2, 2, 2, true>);
