@@ -330,14 +330,15 @@ __device__ __forceinline__ void store_tile(const ProjTable& P, int t, const f32x
   const int j = proj_of(P, t);
   const int Nj = P.n[j];
   const int n = (t - proj_begin(P, j)) * kTileRows + i;
-  uint16_t* Yj = P.y[j];
+  if (n >= Nj) return;
+  // lane's first output row 4a (+16 ct); the rows r of a lane are Nj apart
+  uint16_t* col = P.y[j] + static_cast<size_t>(4 * a) * Nj + n;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      const int m = ct * 16 + 4 * a + r;
-      if (m < M && n < Nj)
-        Yj[static_cast<size_t>(m) * Nj + n] =
+      if (ct * 16 + 4 * a + r < M)
+        col[static_cast<size_t>(ct * 16 + r) * Nj] =
             static_cast<uint16_t>(Act::round(16.0f * total[ct][r]));
     }
 }
@@ -357,7 +358,8 @@ __device__ __forceinline__ float* stream_prologue(u32x4_t* xs, const u32x4_t* (&
   __syncthreads();
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) xrow[ct] = xs + min(ct * 16 + i, M - 1) * pitch;
-  for (int g = wave; g < G; g += kStreamWaves) {
+  const int nw = static_cast<int>(blockDim.x >> 6);
+  for (int g = wave; g < G; g += nw) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       u32x4_t xa[4];
@@ -505,8 +507,9 @@ __device__ __forceinline__ void stream_piece(f32x4_t (&part)[CT], const StreamPi
   }
 }
 
-template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, int HG = 4, bool FULL = true>
-__global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_piece_kernel(
+template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, int HG = 4, bool FULL = true,
+          int WV = kStreamWaves>
+__global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
     const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
   extern __shared__ u32x4_t xs[];
   constexpr int PPU = kUnit / HG;  // pieces per 8-group unit
@@ -516,8 +519,8 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_piece_kernel(
   const int i = lane & 15, a = lane >> 4;
   const int ntiles = P.tile_end[P.count - 1];
   const int H = (G + HG - 1) / HG;  // pieces per tile
-  const int stride = gridDim.x * kStreamWaves;
-  int t = blockIdx.x * kStreamWaves + wave;
+  const int stride = gridDim.x * WV;
+  int t = blockIdx.x * WV + wave;
   const bool active = t < ntiles;
 
   StreamPiece<HG> cur, nxt;
@@ -1402,6 +1405,13 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
     case 3: return launch_gemm<4, 2, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
     case 4: return launch_gemm<2, 4, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
     case 5: return launch_gemm<2, 2, 2, 1, 2, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 6: return launch_gemm<2, 2, 4, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 7: return launch_gemm<1, 2, 4, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 8: return launch_gemm<2, 4, 4, 1, 4, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 10: return launch_gemm<2, 2, 2, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 11: return launch_gemm<1, 2, 8, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 12: return launch_gemm<2, 2, 2, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 13: return launch_gemm<1, 4, 4, 1, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     case 9: return launch_tile<2, 4, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
     default: return launch_gemm<2, 2, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
   }
