@@ -178,16 +178,31 @@ __device__ __forceinline__ float unit_scale(u32x4_t sv, int gg) {
 
 // Stage rows [m0, m0+mrows) x k [k0, k0+kcl) of X into LDS in pair order,
 // row pitch `pitch` 16-byte blocks.
+// Loads go out in batches of 8 per thread before any is waited on.
 __device__ __forceinline__ void stage_activations(u32x4_t* xs, int pitch,
                                                   const uint16_t* __restrict__ X, int K, int m0,
                                                   int mrows, int k0, int kcl) {
+  constexpr int kBatch = 8;
   const int nb = kcl >> 3;
-  for (int t = threadIdx.x; t < mrows * nb; t += blockDim.x) {
-    const int mm = t / nb;
-    const int b = t - mm * nb;
-    const u32x4_t v =
-        *reinterpret_cast<const u32x4_t*>(X + static_cast<size_t>(m0 + mm) * K + k0 + 8 * b);
-    xs[mm * pitch + b] = pair_order(v);
+  const int total = mrows * nb;
+  const int step = static_cast<int>(blockDim.x);
+  for (int base = threadIdx.x; base < total; base += kBatch * step) {
+    u32x4_t v[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int e = min(base + q * step, total - 1);  // clamped: loads stay unconditional
+      const int mm = e / nb;
+      v[q] = *reinterpret_cast<const u32x4_t*>(X + static_cast<size_t>(m0 + mm) * K + k0 +
+                                               8 * (e - mm * nb));
+    }
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int e = base + q * step;
+      if (e < total) {
+        const int mm = e / nb;
+        xs[mm * pitch + (e - mm * nb)] = pair_order(v[q]);
+      }
+    }
   }
 }
 
@@ -866,6 +881,183 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Unit GEMM kernel (prefill chunks): a workgroup of WV waves owns
+// TN = WV * RB * 16 weight rows and TM = CT * 16 activation rows. K is walked
+// one 8-group unit (1024 k) at a time: the unit's activations are staged
+// once into LDS (pair order), the workgroup computes the unit's offset table
+// once (waves split the chains), and every weight is decoded once, by the
+// wave that owns its rows, and feeds CT MFMA column tiles. Weights of a unit
+// are fetched up front (while the activations are staged). The per-output
+// operation sequence is the stream kernel's, so the bits are the same.
+// ---------------------------------------------------------------------------
+
+template <int RB, int CT, int WV, bool PACKED, bool SVEC>
+__global__ __launch_bounds__(WV * 64) void w4a16_gemm_unit_kernel(
+    const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
+    const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, int N, int K, int M) {
+  constexpr int NT = WV * 64;
+  constexpr int TM = CT * 16;
+  constexpr int PB = kUnit * 16 + 1;  // LDS row pitch in 16-byte blocks (padded)
+  constexpr int NBLK = TM * kUnit * 16;  // 16-byte x blocks per unit
+  static_assert(NBLK % NT == 0, "staging must cover the tile exactly");
+  constexpr int BPT = NBLK / NT;  // x blocks staged per thread per unit
+  extern __shared__ u32x4_t xs[];  // [TM][PB], then the offset table
+  float* corr = reinterpret_cast<float*>(xs + TM * PB);  // [kUnit][CT][16]
+
+  const int G = K >> 7;
+  const int U = (G + kUnit - 1) / kUnit;
+  const int ntiles = (N + kTileRows - 1) / kTileRows;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int i = lane & 15, a = lane >> 4;
+  const int m0 = blockIdx.y * TM;
+  const int mrows = min(TM, M - m0);
+
+  int rt[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) rt[rb] = min((blockIdx.x * WV + wave) * RB + rb, ntiles - 1);
+  const bool any_ok = (blockIdx.x * WV + wave) * RB < ntiles;
+
+  // lane addresses of each owned tile at group 0
+  const uint8_t* wbase[RB];
+  const uint8_t* sbase[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    if constexpr (PACKED) {
+      const uint8_t* tile = W + static_cast<size_t>(rt[rb]) * packed_tile_bytes(G);
+      wbase[rb] = tile + lane * 16;
+      sbase[rb] = tile + static_cast<size_t>(G) * 1024 + i * packed_scale_pitch(G);
+    } else {
+      const int row = min(rt[rb] * kTileRows + i, N - 1);
+      wbase[rb] = W + static_cast<size_t>(row) * (K >> 1) + a * 16;
+      sbase[rb] = reinterpret_cast<const uint8_t*>(S + static_cast<size_t>(row) * G);
+    }
+  }
+  constexpr int kStep = PACKED ? 1024 : 64;  // bytes between groups of one lane
+
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t total[RB][CT];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) total[rb][ct] = zero;
+
+  for (int u = 0; u < U; ++u) {
+    const int g0 = u * kUnit;
+    const int gn = min(kUnit, G - g0);
+    // this unit's weights and scales (group indices clamped to G - 1)
+    u32x4_t w[RB][kUnit];
+    uint32_t sc[RB][kUnit / 2];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+      for (int gg = 0; gg < kUnit; ++gg)
+        w[rb][gg] = *reinterpret_cast<const u32x4_t*>(
+            wbase[rb] + static_cast<size_t>(min(g0 + gg, G - 1)) * kStep);
+      if constexpr (PACKED || SVEC) {
+        const u32x4_t sv = *reinterpret_cast<const u32x4_t*>(sbase[rb] + 2 * g0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sc[rb][q] = sv[q];
+      } else {
+        const uint16_t* srow = reinterpret_cast<const uint16_t*>(sbase[rb]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          sc[rb][q] = static_cast<uint32_t>(srow[min(g0 + 2 * q, G - 1)]) |
+                      (static_cast<uint32_t>(srow[min(g0 + 2 * q + 1, G - 1)]) << 16);
+      }
+    }
+    // the unit's activations, rows clamped to the last valid one
+    if (u > 0) __syncthreads();  // previous unit's readers are done
+    {
+      u32x4_t v[BPT];
+#pragma unroll
+      for (int q = 0; q < BPT; ++q) {
+        const int e = threadIdx.x + q * NT;
+        const int mm = e / (kUnit * 16);
+        const int b = e - mm * (kUnit * 16);
+        const int kk = min(g0 * kGroup + 8 * b, K - 8);
+        v[q] = *reinterpret_cast<const u32x4_t*>(
+            X + static_cast<size_t>(m0 + min(mm, mrows - 1)) * K + kk);
+      }
+#pragma unroll
+      for (int q = 0; q < BPT; ++q) {
+        const int e = threadIdx.x + q * NT;
+        const int mm = e / (kUnit * 16);
+        const int b = e - mm * (kUnit * 16);
+        xs[mm * PB + b] = pair_order(v[q]);
+      }
+    }
+    __syncthreads();
+    // offset table of the unit: chains (group, column tile) split over waves
+    for (int c = wave; c < kUnit * CT; c += WV) {
+      const int gg = c / CT, ct = c - gg * CT;
+      u32x4_t xa[4];
+      load_group_x(xa, xs + (ct * 16 + i) * PB + gg * 16, a);
+      const f32x4_t o = group_offset(xa);
+      if (i == 0) *reinterpret_cast<f32x4_t*>(corr + c * 16 + 4 * a) = o;
+    }
+    __syncthreads();
+    if (!any_ok) continue;
+
+    f32x4_t part[RB][CT];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) part[rb][ct] = zero;
+#pragma unroll
+    for (int gg = 0; gg < kUnit; ++gg) {
+      if (gg < gn) {
+        u32x4_t xa[CT][4];
+        f32x4_t t[RB][CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          load_group_x(xa[ct], xs + (ct * 16 + i) * PB + gg * 16, a);
+          const f32x4_t o = *reinterpret_cast<const f32x4_t*>(corr + (gg * CT + ct) * 16 + 4 * a);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) t[rb][ct] = o;
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const u32x4_t B = decode_nibbles(w[rb][gg][d]);
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) t[rb][ct] = mfma16(xa[ct][d], B, t[rb][ct]);
+          }
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          const float s = half_bits_to_f32((sc[rb][gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              part[rb][ct][r] = __builtin_fmaf(s, t[rb][ct][r], part[rb][ct][r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) total[rb][ct] = total[rb][ct] + part[rb][ct];
+  }
+  if (!any_ok) return;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int n = ((blockIdx.x * WV + wave) * RB + rb) * kTileRows + i;
+    if (n >= N) continue;
+    uint16_t* col = Y + static_cast<size_t>(m0 + 4 * a) * N + n;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (ct * 16 + 4 * a + r < mrows)
+          col[static_cast<size_t>(ct * 16 + r) * N] =
+              static_cast<uint16_t>(f32_to_bf16_rne(16.0f * total[rb][ct][r]));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // GEMM kernel (prefill chunks, M >= 33): a workgroup of WN x WM waves owns
 // (WN*RB*16) weight rows x (WM*CT*16) activation rows. K is walked one
 // 128-k group at a time; the group's activation tile sits in one of two LDS
@@ -1380,6 +1572,25 @@ int launch_gemm(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t
   return launch_status();
 }
 
+template <int RB, int CT, int WV, bool PACKED>
+int launch_gemm_unit(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
+                     int K, int M, hipStream_t stream) {
+  constexpr int TM = CT * 16;
+  const size_t lds = static_cast<size_t>(TM) * (kUnit * 16 + 1) * 16 +
+                     static_cast<size_t>(kUnit) * CT * 16 * sizeof(float);
+  const int ntiles = (N + kTileRows - 1) / kTileRows;
+  const int gx = (ntiles + WV * RB - 1) / (WV * RB);
+  const int gy = (M + TM - 1) / TM;
+  if (gy > 65535) return CUDALM_W4A16_ERANGE;
+  const int G = K / kGroup;
+  const bool svec = !PACKED && G % 8 == 0 && aligned(S, 16);
+  auto kern = svec ? w4a16_gemm_unit_kernel<RB, CT, WV, PACKED, true>
+                   : w4a16_gemm_unit_kernel<RB, CT, WV, PACKED, false>;
+  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+  hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(WV * 64), lds, stream, W, S, X, Y, N, K, M);
+  return launch_status();
+}
+
 // Tile-shape override for measurement (CUDALM_W4A16_GEMM_CFG); -1 = by shape.
 int gemm_config() {
   static int cfg = -2;
@@ -1395,9 +1606,10 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
                    int M, hipStream_t stream) {
   int cfg = gemm_config();
   if (cfg < 0) {
-    // 64 x 64 workgroup tiles unless they leave CUs idle; then 64 x 32.
-    const long long wgs = static_cast<long long>((N + 63) / 64) * ((M + 63) / 64);
-    cfg = wgs < cu_count() ? 5 : 0;
+    // unit GEMM: 128 x 32 workgroup tiles of 8 waves while they fill the
+    // CUs, else 64 x 32 tiles of 4 waves
+    const long long wgs = static_cast<long long>((N + 127) / 128) * ((M + 31) / 32);
+    cfg = wgs >= cu_count() ? 24 : 25;
   }
   switch (cfg) {
     case 1: return launch_gemm<2, 2, 2, 2, 1, PACKED>(W, S, X, Y, N, K, M, stream);
@@ -1413,6 +1625,12 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
     case 12: return launch_gemm<2, 2, 2, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
     case 13: return launch_gemm<1, 4, 4, 1, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     case 9: return launch_tile<2, 4, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 20: return launch_gemm_unit<2, 4, 4, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 21: return launch_gemm_unit<1, 4, 8, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 22: return launch_gemm_unit<1, 4, 4, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 23: return launch_gemm_unit<2, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 24: return launch_gemm_unit<1, 2, 8, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 25: return launch_gemm_unit<1, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     default: return launch_gemm<2, 2, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
   }
 }
@@ -1694,7 +1912,7 @@ int cudalm_w4a16_kernel_regs(int variant) {
       return regs_of(w4a16_stream_piece_kernel<true, 1, false, 1, ActBf16, 4, true>);
     case CUDALM_W4A16_VARIANT_TILE16: return regs_of(w4a16_tile_kernel<1, 1, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_TILE32: return regs_of(w4a16_tile_kernel<1, 2, 4, 1, 8, true>);
-    case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_gemm_kernel<2, 2, 2, 2, 2, true>);
+    case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_gemm_unit_kernel<1, 2, 8, true, false>);
     case CUDALM_W4A16_VARIANT_BYTEWISE: return regs_of(w4a16_bytewise_kernel<ActBf16>);
     case CUDALM_W4A16_VARIANT_SPLIT: return regs_of(w4a16_split_kernel<true, 1, false, 1>);
     case CUDALM_W4A16_VARIANT_SWIGLU: return regs_of(w4a16_swiglu_kernel<true, 1, false, 1>);
