@@ -180,15 +180,7 @@ int stream_rows_per_chunk(int K, int M) {
 }
 
 int stream_wgs_per_cu() {
-  static int occ = 0;
-  if (occ == 0) {
-    int v = 4;
-    if (const char* e = getenv("CUDALM_BF16_GEMV_WGS_PER_CU")) {
-      const int p = atoi(e);
-      if (p >= 1 && p <= 32) v = p;
-    }
-    occ = v;
-  }
+  static const int occ = env_setting("CUDALM_BF16_GEMV_WGS_PER_CU", 4, 1, 32);
   return occ;
 }
 

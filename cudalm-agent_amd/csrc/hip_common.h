@@ -6,6 +6,10 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <stdlib.h>
+
+#include <atomic>
+
 #include "cudalm_w4a16.h"
 
 namespace cudalm_hip {
@@ -45,18 +49,27 @@ inline bool aligned(const void* p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
 
-// Compute units of the current device (cached per device).
-inline int cu_count() {
-  static int cached[64] = {0};
+constexpr int kMaxDevices = 64;
+
+inline int current_device() {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
+  return dev;
+}
+
+// Compute units of the current device (cached per device; the cache is
+// filled with relaxed atomics, every writer stores the same value).
+inline int cu_count() {
+  static std::atomic<int> cached[kMaxDevices];
+  const int dev = current_device();
+  if (dev < 0) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 inline int launch_status() {
@@ -64,25 +77,41 @@ inline int launch_status() {
   return e == hipSuccess ? CUDALM_W4A16_OK : CUDALM_W4A16_ELAUNCH;
 }
 
-// Dynamic LDS above 64 KB must be opted into once per kernel.
+// Dynamic LDS above 64 KB must be opted into, per kernel and device. The
+// opt-in is remembered per host thread for up to 64 (device, kernel) pairs;
+// beyond that it is simply repeated.
 template <typename F>
 bool allow_lds(F kernel, size_t bytes) {
   if (bytes <= 64 * 1024) return true;
-  static thread_local const void* done[64] = {nullptr};
+  if (bytes > kLdsMax) return false;
+  struct Entry {
+    const void* fn;
+    int dev;
+  };
+  static thread_local Entry done[64] = {};
+  const void* fn = reinterpret_cast<const void*>(kernel);
+  const int dev = current_device();
   for (auto& d : done) {
-    if (d == reinterpret_cast<const void*>(kernel)) return true;
-    if (d == nullptr) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(bytes > kLdsMax ? bytes : kLdsMax)) != hipSuccess)
+    if (d.fn == fn && d.dev == dev) return true;
+    if (d.fn == nullptr) {
+      if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(kLdsMax)) != hipSuccess)
         return false;
-      d = reinterpret_cast<const void*>(kernel);
+      d = {fn, dev};
       return true;
     }
   }
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                             hipFuncAttributeMaxDynamicSharedMemorySize,
+  return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                              static_cast<int>(kLdsMax)) == hipSuccess;
+}
+
+// Integer setting from the environment, read once (thread-safe static
+// initialization); `fallback` when unset or outside [lo, hi].
+inline int env_setting(const char* name, int fallback, int lo, int hi) {
+  const char* e = getenv(name);
+  if (!e) return fallback;
+  const int v = atoi(e);
+  return (v >= lo && v <= hi) ? v : fallback;
 }
 
 template <typename F>

@@ -1396,24 +1396,12 @@ bool split_fits(int K, int M) { return M <= 32 && split_lds_bytes(K, M) <= kLdsM
 // only): 1 = pieces of 4 groups (default), 2 = pieces of 2 groups, 0 = whole
 // 8-group units. Same bits in every mode.
 int stream_half_enabled() {
-  static int v = -1;
-  if (v < 0) {
-    const char* e = getenv("CUDALM_W4A16_STREAM_PIECE");
-    v = e ? atoi(e) : 1;
-  }
+  static const int v = env_setting("CUDALM_W4A16_STREAM_PIECE", 1, 0, 2);
   return v;
 }
 
 int stream_occupancy() {
-  static int occ = 0;
-  if (occ == 0) {
-    int v = 3;
-    if (const char* e = getenv("CUDALM_W4A16_STREAM_WGS_PER_CU")) {
-      const int p = atoi(e);
-      if (p >= 1 && p <= 32) v = p;
-    }
-    occ = v;
-  }
+  static const int occ = env_setting("CUDALM_W4A16_STREAM_WGS_PER_CU", 3, 1, 32);
   return occ;
 }
 
@@ -1593,11 +1581,7 @@ int launch_gemm_unit(const uint8_t* W, const uint16_t* S, const uint16_t* X, uin
 
 // Tile-shape override for measurement (CUDALM_W4A16_GEMM_CFG); -1 = by shape.
 int gemm_config() {
-  static int cfg = -2;
-  if (cfg == -2) {
-    const char* e = getenv("CUDALM_W4A16_GEMM_CFG");
-    cfg = e ? atoi(e) : -1;
-  }
+  static const int cfg = env_setting("CUDALM_W4A16_GEMM_CFG", -1, -1, 99);
   return cfg;
 }
 
@@ -1612,26 +1596,15 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
     cfg = wgs >= cu_count() ? 24 : 25;
   }
   switch (cfg) {
-    case 1: return launch_gemm<2, 2, 2, 2, 1, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 2: return launch_gemm<2, 2, 2, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 3: return launch_gemm<4, 2, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 4: return launch_gemm<2, 4, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 5: return launch_gemm<2, 2, 2, 1, 2, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 6: return launch_gemm<2, 2, 4, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 7: return launch_gemm<1, 2, 4, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 8: return launch_gemm<2, 4, 4, 1, 4, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 10: return launch_gemm<2, 2, 2, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 11: return launch_gemm<1, 2, 8, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 12: return launch_gemm<2, 2, 2, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 13: return launch_gemm<1, 4, 4, 1, 4, PACKED>(W, S, X, Y, N, K, M, stream);
+    // measurement alternatives: the earlier double-buffered kernel (0), the
+    // tile kernel (9), other unit-GEMM tile shapes (21-23)
+    case 0: return launch_gemm<2, 2, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
     case 9: return launch_tile<2, 4, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 20: return launch_gemm_unit<2, 4, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     case 21: return launch_gemm_unit<1, 4, 8, PACKED>(W, S, X, Y, N, K, M, stream);
     case 22: return launch_gemm_unit<1, 4, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     case 23: return launch_gemm_unit<2, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     case 24: return launch_gemm_unit<1, 2, 8, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 25: return launch_gemm_unit<1, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
-    default: return launch_gemm<2, 2, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
+    default: return launch_gemm_unit<1, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
   }
 }
 
