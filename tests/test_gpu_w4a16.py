@@ -192,6 +192,27 @@ def test_prefill_chunks(w4, orc, dev, N, K, M):
         assert np.array_equal(Y[b], run(w4, w, s, x[b:b + 1], N, K, 1)[0]), b
 
 
+@pytest.mark.parametrize("N,K", [(37, 384), (1023, 1152), (129, 128), (300, 2176)])
+@pytest.mark.parametrize("M", [33, 70, 129])
+def test_prefill_ragged(w4, orc, dev, N, K, M):
+    # the prefill GEMM's partial paths: a last 8-group unit that is short
+    # (K/128 % 8 != 0), scale rows not 16 B aligned in the file layout,
+    # N not a multiple of the 16-row tile and M not a multiple of 32;
+    # file layout, prepacked layout and the tile32 kernel agree bit for bit
+    W, S = orc.synth_w4a16(0x9A61 + N * 3 + K, N, K)
+    X = orc.synth_act(0x9A62 + M, M, K)
+    w, s, x = up(dev, W, S, X)
+    Y = run(w4, w, s, x, N, K, M, "prefill")
+    assert_tol(orc, Y, W, S, X, N, K, M, "prefill_ragged")
+    assert np.array_equal(run(w4, w, s, x, N, K, M, "tile32"), Y)
+    p = w4.repack(w, s, N, K)
+    yp = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    w4.gemv_prepacked(p, x, N, K, M, y=yp, variant="prefill")
+    assert np.array_equal(down(yp).reshape(M, N), Y)
+    for b in (0, M // 2, M - 1):
+        assert np.array_equal(Y[b], run(w4, w, s, x[b:b + 1], N, K, 1)[0]), b
+
+
 def test_lm_head_full_size(w4, orc, dev):
     # N = 248320, K = 1024, M = 1, whole output checked
     N, K = 248320, 1024
