@@ -141,7 +141,7 @@ extern "C" int cudalm_w4a16_repack_host(const uint8_t* weight, const uint16_t* s
   if (!weight || !scale || !packed) return CUDALM_W4A16_ENULL;
   // Layout (the kernels' prepacked form): per 16-row tile, G groups of
   // 1024 weight bytes (lane l = 16a + i: row i, bytes [16a, 16a+16) of the
-  // group), then 16 rows of scales with a pitch of 16 * ceil(G/8) bytes.
+  // group, each dword rotated left by 3 bits), then 16 rows of scales with a pitch of 16 * ceil(G/8) bytes.
   const int G = K / CUDALM_W4A16_GROUP;
   const int SP = 16 * ((G + 7) / 8);
   const std::size_t tile_bytes = static_cast<std::size_t>(G) * 1024 + 16 * static_cast<std::size_t>(SP);
@@ -154,10 +154,18 @@ extern "C" int cudalm_w4a16_repack_host(const uint8_t* weight, const uint16_t* s
         const int n = rt * 16 + (l & 15);
         const int a = l >> 4;
         std::uint8_t* dst = tile + static_cast<std::size_t>(g) * 1024 + 16 * l;
-        if (n < N)
-          std::memcpy(dst, weight + static_cast<std::size_t>(n) * (K / 2) + g * 64 + a * 16, 16);
-        else
+        if (n < N) {
+          // each little-endian dword of 8 nibbles is stored rotated left by 3
+          const std::uint8_t* src = weight + static_cast<std::size_t>(n) * (K / 2) + g * 64 + a * 16;
+          for (int q = 0; q < 4; ++q) {
+            std::uint32_t w;
+            std::memcpy(&w, src + 4 * q, 4);
+            w = (w << 3) | (w >> 29);
+            std::memcpy(dst + 4 * q, &w, 4);
+          }
+        } else {
           std::memset(dst, 0, 16);
+        }
       }
     }
     std::uint8_t* srows = tile + static_cast<std::size_t>(G) * 1024;

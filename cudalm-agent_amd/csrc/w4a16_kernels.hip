@@ -36,7 +36,8 @@
 // batch size or weight layout produced it. The tests pin that.
 //
 // Prepacked ("repacked at load") weight layout, per 16-row tile:
-//   [G x 1024 B weights: group g at g*1024, lane l's 16 bytes at 16*l]
+//   [G x 1024 B weights: group g at g*1024, lane l's 16 bytes at 16*l,
+//    each little-endian dword of 8 nibbles rotated left by 3 bits]
 //   [16 rows x SP B scales: row i at G*1024 + i*SP, fp16 of groups 0..G-1,
 //    SP = 16 * ceil(G/8) (zero padded)]
 // so one wave load of a group is 1 KB contiguous and one 16-byte load
@@ -74,14 +75,33 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
 }
 
 // 8 nibbles (k = 0..7 of a block, nibble k at bits 4k) -> 4 bf16 pairs
-// (k, k+4), each element 1.5 + q/16.
+// (k, k+4), each element 1.5 + q/16. ROT: the dword is the prepacked form,
+// rotated left by 3 at load time, so pair 0 is already in place (one
+// v_bitop3) and pairs 1..3 need one v_alignbit each: 7 VALU ops instead of 8.
+__device__ __forceinline__ uint32_t rotr(uint32_t w, int s) {
+  return __builtin_amdgcn_alignbit(w, w, s);
+}
+
+template <bool ROT = false>
 __device__ __forceinline__ u32x4_t decode_nibbles(uint32_t w) {
   u32x4_t a;
-  a[0] = ((w << 3) & 0x00780078u) ^ 0x3FC03FC0u;
-  a[1] = ((w >> 1) & 0x00780078u) ^ 0x3FC03FC0u;
-  a[2] = ((w >> 5) & 0x00780078u) ^ 0x3FC03FC0u;
-  a[3] = ((w >> 9) & 0x00780078u) ^ 0x3FC03FC0u;
+  if constexpr (ROT) {
+    a[0] = (w & 0x00780078u) ^ 0x3FC03FC0u;
+    a[1] = (rotr(w, 4) & 0x00780078u) ^ 0x3FC03FC0u;
+    a[2] = (rotr(w, 8) & 0x00780078u) ^ 0x3FC03FC0u;
+    a[3] = (rotr(w, 12) & 0x00780078u) ^ 0x3FC03FC0u;
+  } else {
+    a[0] = ((w << 3) & 0x00780078u) ^ 0x3FC03FC0u;
+    a[1] = ((w >> 1) & 0x00780078u) ^ 0x3FC03FC0u;
+    a[2] = ((w >> 5) & 0x00780078u) ^ 0x3FC03FC0u;
+    a[3] = ((w >> 9) & 0x00780078u) ^ 0x3FC03FC0u;
+  }
   return a;
+}
+
+// Prepacked form of a file dword of 8 nibbles (see decode_nibbles<true>).
+__host__ __device__ __forceinline__ uint32_t prepack_dword(uint32_t w) {
+  return (w << 3) | (w >> 29);
 }
 
 // Natural bf16 order [x0x1 x2x3 x4x5 x6x7] -> pair order [x0x4 x1x5 x2x6 x3x7].
@@ -108,21 +128,13 @@ __device__ __forceinline__ f32x4_t group_offset(const u32x4_t (&xa)[4]) {
   return c;
 }
 
-// (1/16) sum_k q x over one group of one 16x16 tile.
-__device__ __forceinline__ f32x4_t group_product(u32x4_t w, const u32x4_t (&xa)[4], f32x4_t corr) {
-  f32x4_t t = mfma16(xa[0], decode_nibbles(w[0]), corr);
-  t = mfma16(xa[1], decode_nibbles(w[1]), t);
-  t = mfma16(xa[2], decode_nibbles(w[2]), t);
-  t = mfma16(xa[3], decode_nibbles(w[3]), t);
-  return t;
-}
-
 // Activation / output element type of a kernel instance. Both encode a
 // weight nibble as the exact value 1.5 + q/16 in the activation's 16-bit
 // format, so the same offset cancellation and epilogue apply.
 struct ActBf16 {
   static constexpr uint32_t kNegOffsetPair = 0xBFC0BFC0u;  // -1.5, -1.5
-  __device__ static u32x4_t decode(uint32_t w) { return decode_nibbles(w); }
+  template <bool ROT>
+  __device__ static u32x4_t decode(uint32_t w) { return decode_nibbles<ROT>(w); }
   __device__ static f32x4_t mma(u32x4_t a, u32x4_t b, f32x4_t c) { return mfma16(a, b, c); }
   __device__ static uint32_t round(float f) { return f32_to_bf16_rne(f); }
   __device__ static float widen(uint32_t h) { return bf16_lo(h); }
@@ -130,15 +142,24 @@ struct ActBf16 {
 
 // fp16: 1.0 = 0x3C00, 10 mantissa bits, so q/16 sits at bit 6 and the
 // biased nibble (q + 8 = nibble ^ 8) lands in bits 6..9: 0x3C00 | 0x0200
-// is 1.5, and nibble k moves to bit 6 of its half with one shift.
+// is 1.5, and nibble k moves to bit 6 of its half with one shift (one
+// rotation from the prepacked form, which is the file dword rotated left 3).
 struct ActF16 {
   static constexpr uint32_t kNegOffsetPair = 0xBE00BE00u;  // -1.5, -1.5
+  template <bool ROT>
   __device__ static u32x4_t decode(uint32_t w) {
     u32x4_t a;
-    a[0] = ((w << 6) & 0x03C003C0u) ^ 0x3E003E00u;
-    a[1] = ((w << 2) & 0x03C003C0u) ^ 0x3E003E00u;
-    a[2] = ((w >> 2) & 0x03C003C0u) ^ 0x3E003E00u;
-    a[3] = ((w >> 6) & 0x03C003C0u) ^ 0x3E003E00u;
+    if constexpr (ROT) {
+      a[0] = (rotr(w, 29) & 0x03C003C0u) ^ 0x3E003E00u;
+      a[1] = (rotr(w, 1) & 0x03C003C0u) ^ 0x3E003E00u;
+      a[2] = (rotr(w, 5) & 0x03C003C0u) ^ 0x3E003E00u;
+      a[3] = (rotr(w, 9) & 0x03C003C0u) ^ 0x3E003E00u;
+    } else {
+      a[0] = ((w << 6) & 0x03C003C0u) ^ 0x3E003E00u;
+      a[1] = ((w << 2) & 0x03C003C0u) ^ 0x3E003E00u;
+      a[2] = ((w >> 2) & 0x03C003C0u) ^ 0x3E003E00u;
+      a[3] = ((w >> 6) & 0x03C003C0u) ^ 0x3E003E00u;
+    }
     return a;
   }
   __device__ static f32x4_t mma(u32x4_t a, u32x4_t b, f32x4_t c) {
@@ -150,6 +171,13 @@ struct ActF16 {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
   }
   __device__ static float widen(uint32_t h) { return half_bits_to_f32(h & 0xFFFFu); }
+};
+
+// An activation trait bound to a weight layout: decode() reads file dwords
+// (PACKED false) or prepacked, rotated dwords (PACKED true).
+template <class Act, bool PACKED>
+struct Layout : Act {
+  __device__ static u32x4_t decode(uint32_t w) { return Act::template decode<PACKED>(w); }
 };
 
 // -1.5 * (sum over the group of this lane-set's activation rows) in the
@@ -430,7 +458,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
     stream_load_t<PACKED, SVEC>(nxt, P, K, G, has_next ? nt : t, has_next ? nu * kUnit : u * kUnit,
                                 lane);
     const int g0 = u * kUnit;
-    stream_unit<NR, CT, Act>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
+    stream_unit<NR, CT, Layout<Act, PACKED>>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       total[ct] = total[ct] + part[ct];
@@ -563,7 +591,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
     // branching around the loads
     stream_load_piece<HG, PACKED, SVEC, FULL>(nxt, anx, G, (has_next ? nh : h) * HG);
     const int g0 = h * HG;
-    stream_piece<HG, NR, CT, Act, FULL>(part, cur, xrow, corr, g0, min(HG, G - g0), a);
+    stream_piece<HG, NR, CT, Layout<Act, PACKED>, FULL>(part, cur, xrow, corr, g0, min(HG, G - g0), a);
     // an 8-group unit ends after its last piece or at the tile's last piece
     if ((h % PPU) == PPU - 1 || h == H - 1) {
 #pragma unroll
@@ -626,7 +654,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
     const int g0 = (sl % U) * kUnit;
-    stream_unit<NR, CT, Act>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
+    stream_unit<NR, CT, Layout<Act, PACKED>>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) slots[(sl * CT + ct) * 64 + lane] = part[ct];
   }
@@ -726,7 +754,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
     const int g0 = (sl % U) * kUnit;
-    stream_unit<NR, CT>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
+    stream_unit<NR, CT, Layout<ActBf16, PACKED>>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) slots[(sl * CT + ct) * 64 + lane] = part[ct];
   }
@@ -838,7 +866,7 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
         for (int d = 0; d < 4; ++d) {
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb) {
-            const u32x4_t B = decode_nibbles(w[gl][rb][d]);
+            const u32x4_t B = decode_nibbles<PACKED>(w[gl][rb][d]);
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) tp[rb][ct] = mfma16(xa[ct][d], B, tp[rb][ct]);
           }
@@ -1020,7 +1048,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_gemm_unit_kernel(
         for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
           for (int d = 0; d < 4; ++d) {
-            const u32x4_t B = decode_nibbles(w[rb][gg][d]);
+            const u32x4_t B = decode_nibbles<PACKED>(w[rb][gg][d]);
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) t[rb][ct] = mfma16(xa[ct][d], B, t[rb][ct]);
           }
@@ -1185,7 +1213,7 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_gemm_kernel(
         for (int d = 0; d < 4; ++d) {
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb) {
-            const u32x4_t B = decode_nibbles(wc[gl][rb][d]);
+            const u32x4_t B = decode_nibbles<PACKED>(wc[gl][rb][d]);
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) tp[rb][ct] = mfma16(xa[ct][d], B, tp[rb][ct]);
           }
@@ -1348,10 +1376,12 @@ __global__ __launch_bounds__(256) void w4a16_repack_kernel(
     }
   }
   u32x4_t v;
-  for (int q = 0; q < 4; ++q)
+  for (int q = 0; q < 4; ++q) {
     v[q] = static_cast<uint32_t>(out[4 * q]) | (static_cast<uint32_t>(out[4 * q + 1]) << 8) |
            (static_cast<uint32_t>(out[4 * q + 2]) << 16) |
            (static_cast<uint32_t>(out[4 * q + 3]) << 24);
+    if (j < G * 64) v[q] = prepack_dword(v[q]);
+  }
   reinterpret_cast<u32x4_t*>(P)[idx] = v;
 }
 

@@ -70,7 +70,8 @@ int cudalm_w4a16_gemv_bf16(const uint8_t* weight, const uint16_t* scale,
 
 /* Bytes of the prepacked (load-time repacked) form of an [N, K] weight,
  * G = K/128: ceil(N/16) * (G * 1024 + 256 * ceil(G/8)). Per 16-row tile:
- * G slabs of 1024 weight bytes (16 bytes per MFMA lane), then the tile's
+ * G slabs of 1024 weight bytes (16 bytes per MFMA lane; each little-endian
+ * dword of 8 nibbles stored rotated left by 3 bits), then the tile's
  * 16 rows of fp16 scales, each row padded to 16 * ceil(G/8) bytes.
  * 0 on invalid shape. */
 size_t cudalm_w4a16_packed_bytes(int N, int K);
