@@ -205,32 +205,62 @@ __device__ __forceinline__ float unit_scale(u32x4_t sv, int gg) {
 }
 
 // Stage rows [m0, m0+mrows) x k [k0, k0+kcl) of X into LDS in pair order,
-// row pitch `pitch` 16-byte blocks.
-// Loads go out in batches of 8 per thread before any is waited on.
-__device__ __forceinline__ void stage_activations(u32x4_t* xs, int pitch,
-                                                  const uint16_t* __restrict__ X, int K, int m0,
-                                                  int mrows, int k0, int kcl) {
-  constexpr int kBatch = 8;
+// row pitch `pitch` 16-byte blocks. Thread t moves the 16-byte blocks
+// e = t + q * blockDim.x; loads go out in batches of up to 8 per thread
+// before any is waited on. A batch is split into stage_load (registers) and
+// stage_store (LDS) so that a kernel can issue its first batch ahead of its
+// weight loads: memory returns in issue order, so x loaded first is usable
+// while the weights are still in flight.
+constexpr int kStageBatch = 8;
+
+struct StageBatch {
+  u32x4_t v[kStageBatch];
+};
+
+// Batch b (blocks [b * 8 * blockDim.x, (b + 1) * 8 * blockDim.x)).
+__device__ __forceinline__ void stage_load(StageBatch& sb, const uint16_t* __restrict__ X, int K,
+                                           int m0, int mrows, int k0, int kcl, int b) {
   const int nb = kcl >> 3;
   const int total = mrows * nb;
   const int step = static_cast<int>(blockDim.x);
-  for (int base = threadIdx.x; base < total; base += kBatch * step) {
-    u32x4_t v[kBatch];
+  const int first = b * kStageBatch * step;  // uniform
 #pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      const int e = min(base + q * step, total - 1);  // clamped: loads stay unconditional
+  for (int q = 0; q < kStageBatch; ++q) {
+    if (first + q * step < total) {  // uniform: whole batches of blocks
+      const int e = min(first + q * step + static_cast<int>(threadIdx.x), total - 1);
       const int mm = e / nb;
-      v[q] = *reinterpret_cast<const u32x4_t*>(X + static_cast<size_t>(m0 + mm) * K + k0 +
-                                               8 * (e - mm * nb));
+      sb.v[q] = *reinterpret_cast<const u32x4_t*>(X + static_cast<size_t>(m0 + mm) * K + k0 +
+                                                  8 * (e - mm * nb));
     }
+  }
+}
+
+__device__ __forceinline__ void stage_store(u32x4_t* xs, int pitch, const StageBatch& sb,
+                                            int mrows, int kcl, int b) {
+  const int nb = kcl >> 3;
+  const int total = mrows * nb;
+  const int step = static_cast<int>(blockDim.x);
+  const int first = b * kStageBatch * step + static_cast<int>(threadIdx.x);
 #pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      const int e = base + q * step;
-      if (e < total) {
-        const int mm = e / nb;
-        xs[mm * pitch + (e - mm * nb)] = pair_order(v[q]);
-      }
+  for (int q = 0; q < kStageBatch; ++q) {
+    const int e = first + q * step;
+    if (e < total) {
+      const int mm = e / nb;
+      xs[mm * pitch + (e - mm * nb)] = pair_order(sb.v[q]);
     }
+  }
+}
+
+// Batches b0.. to the end.
+__device__ __forceinline__ void stage_activations(u32x4_t* xs, int pitch,
+                                                  const uint16_t* __restrict__ X, int K, int m0,
+                                                  int mrows, int k0, int kcl, int b0 = 0) {
+  const int total = mrows * (kcl >> 3);
+  const int per_batch = kStageBatch * static_cast<int>(blockDim.x);
+  for (int b = b0; b * per_batch < total; ++b) {
+    StageBatch sb;
+    stage_load(sb, X, K, m0, mrows, k0, kcl, b);
+    stage_store(xs, pitch, sb, mrows, kcl, b);
   }
 }
 
@@ -393,11 +423,12 @@ __device__ __forceinline__ void store_tile(const ProjTable& P, int t, const f32x
 template <int CT, class Act = ActBf16>
 __device__ __forceinline__ float* stream_prologue(u32x4_t* xs, const u32x4_t* (&xrow)[CT],
                                                   const uint16_t* __restrict__ X, int K, int M,
-                                                  int wave, int i, int a) {
+                                                  int wave, int i, int a, const StageBatch& sb0) {
   const int G = K >> 7;
   const int pitch = (K >> 3) + 1;
   float* corr = reinterpret_cast<float*>(xs + M * pitch);
-  stage_activations(xs, pitch, X, K, 0, M, 0, K);
+  stage_store(xs, pitch, sb0, M, K, 0);
+  stage_activations(xs, pitch, X, K, 0, M, 0, K, 1);
   __syncthreads();
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) xrow[ct] = xs + min(ct * 16 + i, M - 1) * pitch;
@@ -434,11 +465,13 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
   int t = blockIdx.x * kStreamWaves + wave;
   const bool active = t < ntiles;
 
-  // first unit's weights fly while the activations are staged
+  // x's first batch, then the first unit's weights, fly together
+  StageBatch sb0;
+  stage_load(sb0, X, K, 0, M, 0, K, 0);
   StreamUnit cur, nxt;
   stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t, ntiles - 1), 0, lane);
   const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a);
+  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a, sb0);
   if (!active) return;
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -566,11 +599,14 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
   int t = blockIdx.x * WV + wave;
   const bool active = t < ntiles;
 
+  // x's first batch, then the first piece's weights, fly together
+  StageBatch sb0;
+  stage_load(sb0, X, K, 0, M, 0, K, 0);
   StreamPiece<HG> cur, nxt;
   TileAddr acur = tile_addr<PACKED>(P, K, G, min(t, ntiles - 1), lane);
   stream_load_piece<HG, PACKED, SVEC, FULL>(cur, acur, G, 0);
   const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a);
+  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a, sb0);
   if (!active) return;
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -636,14 +672,16 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
   f32x4_t* slots = reinterpret_cast<f32x4_t*>(
       reinterpret_cast<float*>(xs + M * pitch) + G * 16 * CT);
 
-  // this wave's first slot loads fly while the activations are staged
+  // x's first batch, then this wave's first slot loads, fly together
+  StageBatch sb0;
+  stage_load(sb0, X, K, 0, M, 0, K, 0);
   StreamUnit cur;
   {
     const int sl = min(wave, nslots - 1);
     stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t0 + sl / U, ntiles - 1), (sl % U) * kUnit, lane);
   }
   const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a);
+  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a, sb0);
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int sl = wave; sl < nslots; sl += kStreamWaves) {
@@ -741,11 +779,13 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
     const int r = sl % (2 * U);
     stream_load_t<PACKED, SVEC>(u, P, K, G, (r / U) * nt + tf, (r % U) * kUnit, lane);
   };
+  StageBatch sb0;
+  stage_load(sb0, X + static_cast<size_t>(m0) * K, K, 0, mrows, 0, K, 0);
   StreamUnit cur;
   slot_load(cur, min(wave, nslots - 1));
   const u32x4_t* xrow[CT];
   const float* corr =
-      stream_prologue<CT>(xs, xrow, X + static_cast<size_t>(m0) * K, K, mrows, wave, i, a);
+      stream_prologue<CT>(xs, xrow, X + static_cast<size_t>(m0) * K, K, mrows, wave, i, a, sb0);
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int sl = wave; sl < nslots; sl += kStreamWaves) {
