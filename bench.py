@@ -312,6 +312,22 @@ def main():
         del c0
 
     extra = {}
+    # ---------------- small-M batched decode on the LM head (M = 8, 32) ----------------
+    if not args.lm_head_only:
+        small = {}
+        for Mb in (8, 32):
+            xb = synth_act(torch, Mb, K, 0x11B0 + Mb, dev)
+            yb = torch.empty((Mb, N), dtype=torch.bfloat16, device=dev)
+            xbp, ybp = xb.data_ptr(), yb.data_ptr()
+            lb = [(lambda pp=p.data_ptr(): lib.cudalm_w4a16_gemv_bf16_prepacked(pp, xbp, ybp, N, K, Mb, sraw))
+                  for p in packs]
+            _, tot = time_launches(torch, lb, 100, args.warmup, stream)
+            per_b = tot / 100  # back-to-back launches between two events
+            nb = algo_bytes(N, K, Mb)
+            small[f"M{Mb}"] = {"kernel_us": round(per_b * 1e6, 2), "GBps": round(nb / per_b / 1e9, 1),
+                               "frac_hbm_peak": round(nb / per_b / 1e9 / HBM_PEAK_GBS, 4),
+                               "algorithmic_bytes": nb}
+        extra["lm_head_small_m"] = small
     # ---------------- census: 186 projections + LM head per decode step ----------------
     if not args.no_census:
         calls = census_calls()

@@ -1475,28 +1475,46 @@ int stream_occupancy() {
   return occ;
 }
 
+// Workgroups per CU of the 8-wave stream kernel (two column tiles).
+int stream_occupancy_wide() {
+  static const int occ = env_setting("CUDALM_W4A16_STREAM_WIDE_WGS_PER_CU", 2, 1, 8);
+  return occ;
+}
+
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
+  // Two column tiles (M > 16) hold up to 64 KB of x per workgroup, so at
+  // most two workgroups fit a CU: 8-wave workgroups keep 16 waves resident
+  // (measured 3.5 us faster than 4-wave ones on the M = 32 LM head).
+  constexpr int WV = CT == 2 ? 8 : kStreamWaves;
   const size_t lds = stream_lds_bytes(K, M);
   const int ntiles = P.tile_end[P.count - 1];
-  int per_cu = stream_occupancy();
+  int per_cu = CT == 2 ? stream_occupancy_wide() : stream_occupancy();
   const int lds_fit = static_cast<int>(kLdsMax / (lds > 0 ? lds : 1));
   if (lds_fit < per_cu) per_cu = lds_fit > 0 ? lds_fit : 1;
   // Persistent: as many workgroups as stay resident (a tile-count-balanced
   // grid with fewer waves, or one with more than fit, both measured slower
   // on the LM head than this one-round-uneven split).
-  const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
-  const int cap = cu_count() * per_cu;
-  const int grid = want < cap ? want : cap;
   const int G = K / kGroup;
   const int mode = stream_half_enabled();
-  auto kern = mode == 2   ? (G % 2 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, true>
-                                          : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, false>)
-              : mode == 1 ? (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true>
-                                          : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false>)
-                          : w4a16_stream_kernel<PACKED, NR, SVEC, CT, Act>;
+  if (mode == 0) {  // whole-unit kernel (measurement baseline), 4-wave workgroups
+    const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
+    const int cap = cu_count() * per_cu;
+    auto kern = w4a16_stream_kernel<PACKED, NR, SVEC, CT, Act>;
+    if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+    hipLaunchKernelGGL(kern, dim3(want < cap ? want : cap), dim3(kStreamWaves * 64), lds, stream,
+                       P, X, K, M);
+    return launch_status();
+  }
+  const int want = (ntiles + WV - 1) / WV;
+  const int cap = cu_count() * per_cu;
+  const int grid = want < cap ? want : cap;
+  auto kern = mode == 2 ? (G % 2 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, true, WV>
+                                      : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, false, WV>)
+                        : (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV>
+                                      : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV>);
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(kStreamWaves * 64), lds, stream, P, X, K, M);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M);
   return launch_status();
 }
 
