@@ -100,7 +100,10 @@ def _numpy_repack(W, S, N, K):
             i, a = lane & 15, lane >> 4
             rows = Wp[rt * 16 + i].reshape(G, 64)
             wpart[:, lane, :] = rows[:, a * 16:a * 16 + 16]
-        tiles.append(np.concatenate([wpart.ravel(), Sp[rt * 16:rt * 16 + 16].view(np.uint8).ravel()]))
+        # each little-endian dword of 8 nibbles is stored rotated left by 3 bits
+        d = wpart.reshape(-1).view("<u4")
+        d = ((d << np.uint32(3)) | (d >> np.uint32(29))).astype("<u4")
+        tiles.append(np.concatenate([d.view(np.uint8), Sp[rt * 16:rt * 16 + 16].view(np.uint8).ravel()]))
     return np.concatenate(tiles)
 
 
