@@ -209,11 +209,15 @@ def main():
                     help="headline workload only (for counter collection)")
     ap.add_argument("--bf16-lm-head-only", action="store_true",
                     help="only the tied bf16 LM head lines (for counter collection)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="headline plus the M = 512 prefill lines (for counter collection)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (x5), to scale HBM counters")
     args = ap.parse_args()
     if args.lm_head_only:
         args.no_census = args.no_prefill = args.no_cpu = args.no_next = True
+    if args.prefill_only:
+        args.no_census = args.no_cpu = args.no_next = True
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the W4A16 projection path runs on a single "
