@@ -231,6 +231,25 @@ def test_lm_head_full_size(w4, orc, dev):
     assert np.array_equal(orc.bf16_to_f32(Y2), orc.bf16_to_f32(Y) * 2)
 
 
+@pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
+def test_nonfinite_activation(w4, orc, dev, bad):
+    # every output sums over every k, so one non-finite x[k] makes every
+    # output of that row non-finite in the reference (ref_gemv_bf16 gives
+    # +-Inf or NaN); the 1.5 offset cancellation gives NaN for an infinity.
+    # Other batch rows are untouched (row independence).
+    N, K, M = 512, 1024, 3
+    W, S, X = orc.fixture_kind("random", 0x51, N, K, M)
+    Xb = X.copy()
+    Xb[1, 77] = orc.f32_to_bf16(np.array([bad], np.float32))[0]
+    w, s, x = up(dev, W, S, Xb)
+    for variant in ("auto", "stream", "tile16", "prefill"):
+        Y = run(w4, w, s, x, N, K, M, variant)
+        Yf = orc.bf16_to_f32(Y)
+        assert not np.isfinite(Yf[1]).any(), variant
+        Y0 = run(w4, *up(dev, W, S, X), N, K, M, variant)
+        assert np.array_equal(Y[[0, 2]], Y0[[0, 2]]), variant
+
+
 def test_repack_device_equals_host(w4, orc, dev):
     for N, K in ((1, 128), (37, 384), (1023, 1024), (16, 3584)):
         W, S, _ = orc.fixture_gemv(N * 7 + K, N, K)
