@@ -148,6 +148,22 @@ def time_launches(torch, launches, reps: int, warmup: int, stream):
     return per, t0.elapsed_time(t1) * 1e-3
 
 
+def stream_time(torch, launches, reps: int, warmup: int, stream):
+    """Seconds per launch: `reps` launches back to back (round-robin over
+    `launches`) between two HIP events on `stream`, after `warmup`."""
+    for i in range(warmup):
+        launches[i % len(launches)]()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(reps):
+        launches[i % len(launches)]()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e-3 / reps
+
+
 def graph_time(torch, fn, reps: int, stream):
     """Capture fn() into a HIP graph, replay `reps` times; seconds per replay."""
     g = torch.cuda.CUDAGraph()
@@ -325,8 +341,7 @@ def main():
             xbp, ybp = xb.data_ptr(), yb.data_ptr()
             lb = [(lambda pp=p.data_ptr(): lib.cudalm_w4a16_gemv_bf16_prepacked(pp, xbp, ybp, N, K, Mb, sraw))
                   for p in packs]
-            _, tot = time_launches(torch, lb, 100, args.warmup, stream)
-            per_b = tot / 100  # back-to-back launches between two events
+            per_b = stream_time(torch, lb, 100, args.warmup, stream)
             nb = algo_bytes(N, K, Mb)
             small[f"M{Mb}"] = {"kernel_us": round(per_b * 1e6, 2), "GBps": round(nb / per_b / 1e9, 1),
                                "frac_hbm_peak": round(nb / per_b / 1e9 / HBM_PEAK_GBS, 4),
