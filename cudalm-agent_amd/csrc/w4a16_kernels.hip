@@ -949,37 +949,50 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Unit GEMM kernel (prefill chunks): a workgroup of WV waves owns
+// Unit GEMM kernel (prefill chunks): a k-slice of WV waves owns
 // TN = WV * RB * 16 weight rows and TM = CT * 16 activation rows. K is walked
 // one 8-group unit (1024 k) at a time: the unit's activations are staged
-// once into LDS (pair order), the workgroup computes the unit's offset table
+// once into LDS (pair order), the slice computes the unit's offset table
 // once (waves split the chains), and every weight is decoded once, by the
 // wave that owns its rows, and feeds CT MFMA column tiles. Weights of a unit
 // are fetched up front (while the activations are staged). The per-output
 // operation sequence is the stream kernel's, so the bits are the same.
+//
+// KS > 1 k-slices split the units of the same output tile: slice s takes
+// units s, s + KS, ... with its own LDS buffers, keeps each unit partial,
+// and at the end the partials meet in LDS and are summed in unit order, so
+// the bits do not depend on KS. This serves few-tile, long-K shapes
+// (N = 1024, K = 2048 / 3584), where one slice would walk every unit alone.
 // ---------------------------------------------------------------------------
 
-template <int RB, int CT, int WV, bool PACKED, bool SVEC>
-__global__ __launch_bounds__(WV * 64) void w4a16_gemm_unit_kernel(
+constexpr int kSliceMaxUnits = 4;  // units per k-slice kept as partials (KS > 1)
+
+template <int RB, int CT, int WV, bool PACKED, bool SVEC, int KS = 1>
+__global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
     const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
     const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, int N, int K, int M) {
-  constexpr int NT = WV * 64;
+  constexpr int NT = WV * 64;  // threads of one k-slice
   constexpr int TM = CT * 16;
   constexpr int PB = kUnit * 16 + 1;  // LDS row pitch in 16-byte blocks (padded)
   constexpr int NBLK = TM * kUnit * 16;  // 16-byte x blocks per unit
   static_assert(NBLK % NT == 0, "staging must cover the tile exactly");
   constexpr int BPT = NBLK / NT;  // x blocks staged per thread per unit
-  extern __shared__ u32x4_t xs[];  // [TM][PB], then the offset table
-  float* corr = reinterpret_cast<float*>(xs + TM * PB);  // [kUnit][CT][16]
+  constexpr int XB = TM * PB;     // 16-byte blocks of one slice's x buffer
+  constexpr int NPART = KS == 1 ? 1 : kSliceMaxUnits;
+  extern __shared__ u32x4_t lds[];  // [KS][TM][PB] x, then [KS] offset tables
 
   const int G = K >> 7;
   const int U = (G + kUnit - 1) / kUnit;
   const int ntiles = (N + kTileRows - 1) / kTileRows;
   const int lane = threadIdx.x & 63;
-  const int wave = wave_id();
+  const int slice = KS == 1 ? 0 : wave_id() / WV;
+  const int wave = wave_id() - slice * WV;  // wave within the slice
+  const int tid = static_cast<int>(threadIdx.x) - slice * NT;
   const int i = lane & 15, a = lane >> 4;
   const int m0 = blockIdx.y * TM;
   const int mrows = min(TM, M - m0);
+  u32x4_t* xs = lds + slice * XB;
+  float* corr = reinterpret_cast<float*>(lds + KS * XB) + slice * (kUnit * CT * 16);
 
   int rt[RB];
 #pragma unroll
@@ -1004,15 +1017,21 @@ __global__ __launch_bounds__(WV * 64) void w4a16_gemm_unit_kernel(
   constexpr int kStep = PACKED ? 1024 : 64;  // bytes between groups of one lane
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f32x4_t total[RB][CT];
+  // KS == 1: the running unit sum; KS > 1: this slice's unit partials
+  f32x4_t acc[NPART][RB][CT];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+  for (int q = 0; q < NPART; ++q)
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) total[rb][ct] = zero;
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) acc[q][rb][ct] = zero;
 
-  for (int u = 0; u < U; ++u) {
-    const int g0 = u * kUnit;
-    const int gn = min(kUnit, G - g0);
+  const int iters = (U + KS - 1) / KS;
+  for (int it = 0; it < iters; ++it) {
+    const int u = it * KS + slice;
+    const int uc = min(u, U - 1);  // a slice past the last unit re-reads it and skips the math
+    const int g0 = uc * kUnit;
+    const int gn = u < U ? min(kUnit, G - g0) : 0;
     // this unit's weights and scales (group indices clamped to G - 1)
     u32x4_t w[RB][kUnit];
     uint32_t sc[RB][kUnit / 2];
@@ -1035,12 +1054,12 @@ __global__ __launch_bounds__(WV * 64) void w4a16_gemm_unit_kernel(
       }
     }
     // the unit's activations, rows clamped to the last valid one
-    if (u > 0) __syncthreads();  // previous unit's readers are done
+    if (it > 0) __syncthreads();  // previous unit's readers are done
     {
       u32x4_t v[BPT];
 #pragma unroll
       for (int q = 0; q < BPT; ++q) {
-        const int e = threadIdx.x + q * NT;
+        const int e = tid + q * NT;
         const int mm = e / (kUnit * 16);
         const int b = e - mm * (kUnit * 16);
         const int kk = min(g0 * kGroup + 8 * b, K - 8);
@@ -1049,7 +1068,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_gemm_unit_kernel(
       }
 #pragma unroll
       for (int q = 0; q < BPT; ++q) {
-        const int e = threadIdx.x + q * NT;
+        const int e = tid + q * NT;
         const int mm = e / (kUnit * 16);
         const int b = e - mm * (kUnit * 16);
         xs[mm * PB + b] = pair_order(v[q]);
@@ -1104,10 +1123,54 @@ __global__ __launch_bounds__(WV * 64) void w4a16_gemm_unit_kernel(
         }
       }
     }
+    if constexpr (KS == 1) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[0][rb][ct] = acc[0][rb][ct] + part[rb][ct];
+    } else {
+#pragma unroll
+      for (int q = 0; q < NPART; ++q)
+        if (q == it)
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) acc[q][rb][ct] = part[rb][ct];
+    }
+  }
+
+  f32x4_t total[RB][CT];
+  if constexpr (KS == 1) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) total[rb][ct] = total[rb][ct] + part[rb][ct];
+      for (int ct = 0; ct < CT; ++ct) total[rb][ct] = acc[0][rb][ct];
+  } else {
+    // unit partials meet in LDS (over the x buffers): slot [u][wave][rb][ct][lane]
+    __syncthreads();
+    f32x4_t* slots = reinterpret_cast<f32x4_t*>(lds);
+    if (any_ok) {
+#pragma unroll
+      for (int q = 0; q < NPART; ++q) {
+        const int u = q * KS + slice;
+        if (q < iters && u < U)
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+              slots[(((u * WV + wave) * RB + rb) * CT + ct) * 64 + lane] = acc[q][rb][ct];
+      }
+    }
+    __syncthreads();
+    if (slice != 0) return;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        total[rb][ct] = zero;
+        for (int u = 0; u < U; ++u)
+          total[rb][ct] = total[rb][ct] + slots[(((u * WV + wave) * RB + rb) * CT + ct) * 64 + lane];
+      }
   }
   if (!any_ok) return;
 #pragma unroll
@@ -1648,22 +1711,30 @@ int launch_gemm(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t
   return launch_status();
 }
 
-template <int RB, int CT, int WV, bool PACKED>
+template <int RB, int CT, int WV, bool PACKED, int KS = 1>
 int launch_gemm_unit(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                      int K, int M, hipStream_t stream) {
   constexpr int TM = CT * 16;
-  const size_t lds = static_cast<size_t>(TM) * (kUnit * 16 + 1) * 16 +
-                     static_cast<size_t>(kUnit) * CT * 16 * sizeof(float);
+  const size_t xbytes = static_cast<size_t>(TM) * (kUnit * 16 + 1) * 16;
+  const size_t lds = KS * (xbytes + static_cast<size_t>(kUnit) * CT * 16 * sizeof(float));
+  const int G = K / kGroup;
+  if constexpr (KS > 1) {
+    // every slice keeps at most kSliceMaxUnits partials, and all of them
+    // must fit the x buffers they are parked in
+    const int U = (G + kUnit - 1) / kUnit;
+    if (U > KS * kSliceMaxUnits ||
+        static_cast<size_t>(U) * WV * RB * CT * 64 * 16 > KS * xbytes)
+      return launch_gemm_unit<RB, CT, WV, PACKED, 1>(W, S, X, Y, N, K, M, stream);
+  }
   const int ntiles = (N + kTileRows - 1) / kTileRows;
   const int gx = (ntiles + WV * RB - 1) / (WV * RB);
   const int gy = (M + TM - 1) / TM;
   if (gy > 65535) return CUDALM_W4A16_ERANGE;
-  const int G = K / kGroup;
   const bool svec = !PACKED && G % 8 == 0 && aligned(S, 16);
-  auto kern = svec ? w4a16_gemm_unit_kernel<RB, CT, WV, PACKED, true>
-                   : w4a16_gemm_unit_kernel<RB, CT, WV, PACKED, false>;
+  auto kern = svec ? w4a16_gemm_unit_kernel<RB, CT, WV, PACKED, true, KS>
+                   : w4a16_gemm_unit_kernel<RB, CT, WV, PACKED, false, KS>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-  hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(WV * 64), lds, stream, W, S, X, Y, N, K, M);
+  hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(WV * KS * 64), lds, stream, W, S, X, Y, N, K, M);
   return launch_status();
 }
 
@@ -1679,19 +1750,22 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
   int cfg = gemm_config();
   if (cfg < 0) {
     // unit GEMM: 128 x 32 workgroup tiles of 8 waves while they fill the
-    // CUs, else 64 x 32 tiles of 4 waves
+    // CUs, else 64 x 32 tiles of 4 waves, with two k-slices of 4 waves when
+    // K spans several units (1024x3584 at M = 512: 16.7 -> 14.6 us)
     const long long wgs = static_cast<long long>((N + 127) / 128) * ((M + 31) / 32);
-    cfg = wgs >= cu_count() ? 24 : 25;
+    cfg = wgs >= cu_count() ? 24 : (K > kUnit * kGroup ? 30 : 25);
   }
   switch (cfg) {
     // measurement alternatives: the earlier double-buffered kernel (0), the
-    // tile kernel (9), other unit-GEMM tile shapes (21-23)
+    // tile kernel (9), other unit-GEMM tile shapes (21-23); 30 is the
+    // two-k-slice unit GEMM
     case 0: return launch_gemm<2, 2, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
     case 9: return launch_tile<2, 4, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
     case 21: return launch_gemm_unit<1, 4, 8, PACKED>(W, S, X, Y, N, K, M, stream);
     case 22: return launch_gemm_unit<1, 4, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     case 23: return launch_gemm_unit<2, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     case 24: return launch_gemm_unit<1, 2, 8, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 30: return launch_gemm_unit<1, 2, 4, PACKED, 2>(W, S, X, Y, N, K, M, stream);
     default: return launch_gemm_unit<1, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
   }
 }
