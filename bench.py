@@ -200,7 +200,7 @@ def bench_bf16_lm_head(torch, lib, dev, stream, sraw, reps: int = 40):
         xbp, ybp = xb.data_ptr(), yb.data_ptr()
         L = [(lambda ep=e.data_ptr(): lib.cudalm_bf16_gemv(ep, xbp, ybp, Nb, Kb, Mb, sraw))
              for e in embs]
-        per, _ = time_launches(torch, L, reps, 8, stream)
+        per = stream_time(torch, L, reps, 8, stream)
         byts = 2 * Nb * Kb + 2 * Mb * Kb + 2 * Mb * Nb
         bf[f"M{Mb}"] = {"kernel_us": round(per * 1e6, 2), "GBps": round(byts / per / 1e9, 1),
                         "frac_hbm_peak": round(byts / per / 1e9 / HBM_PEAK_GBS, 4),
@@ -310,8 +310,8 @@ def main():
 
     file_per = float("nan")
     if not args.lm_head_only:
-        file_per, _ = time_launches(torch, [mk_file(w, s) for w, s in zip(ws, ss)],
-                                min(args.steps, 100), args.warmup, stream)
+        file_per = stream_time(torch, [mk_file(w, s) for w, s in zip(ws, ss)],
+                               min(args.steps, 100), args.warmup, stream)
     file_gbs = nbytes / file_per / 1e9 if file_per == file_per else None
 
     # M = 1, N = 3584, K = 1024 (rotate 64 copies = 120 MB; a
@@ -451,7 +451,7 @@ def main():
         L = [(lambda pp=p.data_ptr(): lib.cudalm_w4a16_gemv_f16_prepacked(pp, xh16.data_ptr(),
                                                                           yh16.data_ptr(), N, K, 1,
                                                                           sraw)) for p in packs]
-        per, _ = time_launches(torch, L, 40, 8, stream)
+        per = stream_time(torch, L, 100, 8, stream)
         nxt["f16_twin_lm_head_M1"] = {"kernel_us": round(per * 1e6, 2),
                                       "GBps": round(nbytes / per / 1e9, 1)}
         extra["next_rows"] = nxt
