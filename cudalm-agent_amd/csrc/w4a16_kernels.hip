@@ -586,17 +586,21 @@ __device__ __forceinline__ void stream_piece(f32x4_t (&part)[CT], const StreamPi
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, int HG = 4, bool FULL = true,
           int WV = kStreamWaves>
 __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
-    const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
+    const ProjTable P, const uint16_t* __restrict__ X, int K, int M, int pwg, int t_static) {
   extern __shared__ u32x4_t xs[];
   constexpr int PPU = kUnit / HG;  // pieces per 8-group unit
   const int G = K >> 7;
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   const int i = lane & 15, a = lane >> 4;
-  const int ntiles = P.tile_end[P.count - 1];
   const int H = (G + HG - 1) / HG;  // pieces per tile
-  const int stride = gridDim.x * WV;
-  int t = blockIdx.x * WV + wave;
+  // Workgroups [0, pwg) are persistent and stride over tiles [0, t_static);
+  // the rest take one tile per wave of [t_static, ntiles) and are dispatched
+  // as persistent workgroups retire.
+  const bool persistent = static_cast<int>(blockIdx.x) < pwg;
+  const int ntiles = persistent ? t_static : P.tile_end[P.count - 1];
+  const int stride = persistent ? pwg * WV : ntiles;
+  int t = persistent ? blockIdx.x * WV + wave : t_static + (blockIdx.x - pwg) * WV + wave;
   const bool active = t < ntiles;
 
   // x's first batch, then the first piece's weights, fly together
@@ -1538,6 +1542,13 @@ int stream_occupancy() {
   return occ;
 }
 
+// Share of the tiles (per mille) left to dispatcher-balanced workgroups
+// after the persistent ones (CUDALM_W4A16_STREAM_TAIL; 0 = all static).
+int stream_tail_permille() {
+  static const int v = env_setting("CUDALM_W4A16_STREAM_TAIL", 150, 0, 900);
+  return v;
+}
+
 // Workgroups per CU of the 8-wave stream kernel (two column tiles).
 int stream_occupancy_wide() {
   static const int occ = env_setting("CUDALM_W4A16_STREAM_WIDE_WGS_PER_CU", 2, 1, 8);
@@ -1571,13 +1582,26 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   }
   const int want = (ntiles + WV - 1) / WV;
   const int cap = cu_count() * per_cu;
-  const int grid = want < cap ? want : cap;
+  const int pwg = want < cap ? want : cap;
+  int t_static = ntiles, grid = pwg;
+  // Dispatcher-balanced tail: waves of a static grid finish up to ~4 us
+  // apart on the LM head (XCDs stream at different rates), and for the last
+  // microseconds too few loads are in flight. Handing the last 15% of the
+  // tiles to workgroups that the dispatcher places as persistent ones retire
+  // evens that out: LM head 27.5 -> 25.6 us at M = 1, 30.1 -> 29.7 us at
+  // M = 8; at M >= 16 the tail workgroups' larger x staging makes it slower.
+  const int tail_pm = M <= 8 ? stream_tail_permille() : 0;
+  const int tail = static_cast<int>(static_cast<long long>(ntiles) * tail_pm / 1000);
+  if (tail > 0 && ntiles - tail > pwg * WV) {
+    t_static = ntiles - tail;
+    grid = pwg + (tail + WV - 1) / WV;
+  }
   auto kern = mode == 2 ? (G % 2 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, true, WV>
                                       : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, false, WV>)
                         : (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV>
                                       : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV>);
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M, pwg, t_static);
   return launch_status();
 }
 
