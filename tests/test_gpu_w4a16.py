@@ -250,6 +250,26 @@ def test_nonfinite_activation(w4, orc, dev, bad):
         assert np.array_equal(Y[[0, 2]], Y0[[0, 2]]), variant
 
 
+@pytest.mark.parametrize("N,M", [(248320, 8), (100003, 3), (100003, 1), (248320, 32)])
+def test_large_n_small_m(w4, orc, dev, N, M):
+    # launches large enough for the dispatcher-placed tail workgroups
+    # (M <= 8; N = 100003 leaves a ragged last tile and a partial last tail
+    # workgroup) and for the 8-wave two-column-tile grid (M = 32): tolerance
+    # against the oracle, both layouts equal, and row b == the M = 1 call
+    K = 1024
+    W, S = orc.synth_w4a16(0x7A11 + N + M, N, K)
+    X = orc.synth_act(0x7A12 + M, M, K)
+    w, s, x = up(dev, W, S, X)
+    Y = run(w4, w, s, x, N, K, M)
+    st = assert_tol(orc, Y, W, S, X, N, K, M, "large_n")
+    assert st["n_over_2ulp"] <= max(1, st["n"] // 10000)
+    p = w4.repack(w, s, N, K)
+    yp = w4.gemv_prepacked(p, x, N, K, M)
+    assert np.array_equal(down(yp).reshape(M, N), Y)
+    for b in sorted({0, M // 2, M - 1}):
+        assert np.array_equal(Y[b], run(w4, w, s, x[b:b + 1], N, K, 1)[0]), b
+
+
 def test_repack_device_equals_host(w4, orc, dev):
     for N, K in ((1, 128), (37, 384), (1023, 1024), (16, 3584)):
         W, S, _ = orc.fixture_gemv(N * 7 + K, N, K)
