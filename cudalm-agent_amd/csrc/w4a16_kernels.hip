@@ -1193,187 +1193,6 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// GEMM kernel (prefill chunks, M >= 33): a workgroup of WN x WM waves owns
-// (WN*RB*16) weight rows x (WM*CT*16) activation rows. K is walked one
-// 128-k group at a time; the group's activation tile sits in one of two LDS
-// buffers while the next group's activations and weights are loaded into
-// registers, so each group costs one barrier and its loads overlap the
-// previous group's MFMAs.
-// ---------------------------------------------------------------------------
-
-template <int RB, int CT, int WN, int WM, int GPI, bool PACKED>
-__global__ __launch_bounds__(WN * WM * 64) void w4a16_gemm_kernel(
-    const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
-    const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, int N, int K, int M) {
-  constexpr int NT = WN * WM * 64;
-  constexpr int CM = WM * CT * 16;           // activation rows per workgroup
-  constexpr int BPR = 16 * GPI;              // 16-byte blocks per row per iteration
-  constexpr int PB = BPR + 1;                // LDS row pitch in blocks (padded)
-  constexpr int TPR = BPR < NT ? BPR : NT;   // threads per staged row
-  constexpr int RPP = NT / TPR;              // rows staged per pass
-  constexpr int BPT = BPR / TPR;             // blocks per thread per row
-  constexpr int NPASS = CM / RPP;            // staging passes per iteration
-  static_assert(CM % RPP == 0 && BPR % TPR == 0, "staging must cover the tile exactly");
-  static_assert(kUnit % GPI == 0, "iterations must not straddle an 8-group unit");
-  extern __shared__ u32x4_t xs[];            // [2][CM][PB]
-  const int G = K >> 7;
-  const int ntiles = (N + kTileRows - 1) / kTileRows;
-  const int lane = threadIdx.x & 63;
-  const int wave = wave_id();
-  const int wn = wave % WN, wm = wave / WN;
-  const int i = lane & 15, a = lane >> 4;
-  const int m0 = blockIdx.y * CM;
-
-  int rt[RB];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) rt[rb] = min((blockIdx.x * WN + wn) * RB + rb, ntiles - 1);
-  const bool any_ok = (blockIdx.x * WN + wn) * RB < ntiles;
-
-  // staging: thread -> (blocks sb + TPR * j of the iteration, rows sr + RPP * pass)
-  const int sb = threadIdx.x % TPR;
-  const int sr = threadIdx.x / TPR;
-  const uint16_t* xsrc[NPASS];
-#pragma unroll
-  for (int q = 0; q < NPASS; ++q)
-    xsrc[q] = X + static_cast<size_t>(min(m0 + sr + RPP * q, M - 1)) * K + 8 * sb;
-
-  // group indices are clamped to G - 1 so the loads are straight-line
-  auto load_w = [&](u32x4_t (&w)[GPI][RB], float (&s)[GPI][RB], int g0) {
-#pragma unroll
-    for (int gl = 0; gl < GPI; ++gl) {
-      const int g = min(g0 + gl, G - 1);
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        if constexpr (PACKED) {
-          const uint8_t* tile = W + static_cast<size_t>(rt[rb]) * packed_tile_bytes(G);
-          w[gl][rb] = *reinterpret_cast<const u32x4_t*>(tile + static_cast<size_t>(g) * 1024 + lane * 16);
-          s[gl][rb] = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(
-              tile + static_cast<size_t>(G) * 1024 + i * packed_scale_pitch(G) + 2 * g));
-        } else {
-          const int row = min(rt[rb] * kTileRows + i, N - 1);
-          w[gl][rb] = *reinterpret_cast<const u32x4_t*>(W + static_cast<size_t>(row) * (K >> 1) +
-                                                        g * 64 + a * 16);
-          s[gl][rb] = half_bits_to_f32(S[static_cast<size_t>(row) * G + g]);
-        }
-      }
-    }
-  };
-  auto load_x = [&](u32x4_t (&v)[NPASS][BPT], int g0) {
-    const int kmax = K - 8;
-#pragma unroll
-    for (int q = 0; q < NPASS; ++q)
-#pragma unroll
-      for (int j = 0; j < BPT; ++j)
-        v[q][j] = *reinterpret_cast<const u32x4_t*>(
-            xsrc[q] + min(g0 * kGroup + 8 * TPR * j, kmax - 8 * sb));
-  };
-  auto store_x = [&](const u32x4_t (&v)[NPASS][BPT], int buf) {
-#pragma unroll
-    for (int q = 0; q < NPASS; ++q)
-#pragma unroll
-      for (int j = 0; j < BPT; ++j)
-        xs[(buf * CM + sr + RPP * q) * PB + sb + TPR * j] = pair_order(v[q][j]);
-  };
-
-  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f32x4_t acc[RB][CT], total[RB][CT];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) acc[rb][ct] = total[rb][ct] = zero;
-
-  u32x4_t wc[GPI][RB];
-  float sc[GPI][RB];
-  {
-    u32x4_t xv[NPASS][BPT];
-    load_x(xv, 0);
-    load_w(wc, sc, 0);
-    store_x(xv, 0);
-  }
-  __syncthreads();
-
-  for (int g0 = 0; g0 < G; g0 += GPI) {
-    const int buf = (g0 / GPI) & 1;
-    const bool more = g0 + GPI < G;
-    u32x4_t xv[NPASS][BPT], wn_[GPI][RB];
-    float sn[GPI][RB];
-    if (more) {
-      load_x(xv, g0 + GPI);
-      load_w(wn_, sn, g0 + GPI);
-    }
-    const int ng = min(GPI, G - g0);
-#pragma unroll
-    for (int gl = 0; gl < GPI; ++gl) {
-      if (gl < ng) {
-        // activation operands of this wave's CT column tiles, and their offsets
-        u32x4_t xa[CT][4];
-        f32x4_t tp[RB][CT];
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          const u32x4_t* xr = xs + (buf * CM + wm * CT * 16 + ct * 16 + i) * PB + gl * 16;
-          load_group_x(xa[ct], xr, a);
-          const f32x4_t c = group_offset(xa[ct]);
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb) tp[rb][ct] = c;
-        }
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb) {
-            const u32x4_t B = decode_nibbles<PACKED>(wc[gl][rb][d]);
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) tp[rb][ct] = mfma16(xa[ct][d], B, tp[rb][ct]);
-          }
-        }
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              acc[rb][ct][r] = __builtin_fmaf(sc[gl][rb], tp[rb][ct][r], acc[rb][ct][r]);
-      }
-    }
-    if ((g0 + GPI) % kUnit == 0 || g0 + ng == G) {
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          total[rb][ct] = total[rb][ct] + acc[rb][ct];
-          acc[rb][ct] = zero;
-        }
-    }
-    if (more) {
-      store_x(xv, buf ^ 1);
-#pragma unroll
-      for (int gl = 0; gl < GPI; ++gl)
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          wc[gl][rb] = wn_[gl][rb];
-          sc[gl][rb] = sn[gl][rb];
-        }
-    }
-    __syncthreads();
-  }
-
-  if (!any_ok) return;
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int n = ((blockIdx.x * WN + wn) * RB + rb) * kTileRows + i;
-    if (n >= N) continue;
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * CT * 16 + ct * 16 + 4 * a + r;
-        if (m < M)
-          Y[static_cast<size_t>(m) * N + n] =
-              static_cast<uint16_t>(f32_to_bf16_rne(16.0f * total[rb][ct][r]));
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Byte-wise fallback for misaligned bases (reference: int4gemv_scalar_bf16_
 // kernel, src/kernels/int4_gemv_bf16.cu:174-213): one wave per (row, m),
 // byte loads only, terms (q*s)*x in k order per lane, wave reduction.
@@ -1720,21 +1539,6 @@ int launch_tile(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t
   return launch_status();
 }
 
-template <int RB, int CT, int WN, int WM, int GPI, bool PACKED>
-int launch_gemm(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N, int K,
-                int M, hipStream_t stream) {
-  constexpr int CM = WM * CT * 16;
-  const size_t lds = static_cast<size_t>(2) * CM * (16 * GPI + 1) * 16;
-  const int ntiles = (N + kTileRows - 1) / kTileRows;
-  const int gx = (ntiles + WN * RB - 1) / (WN * RB);
-  const int gy = (M + CM - 1) / CM;
-  if (gy > 65535) return CUDALM_W4A16_ERANGE;
-  auto kern = w4a16_gemm_kernel<RB, CT, WN, WM, GPI, PACKED>;
-  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-  hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(WN * WM * 64), lds, stream, W, S, X, Y, N, K, M);
-  return launch_status();
-}
-
 template <int RB, int CT, int WV, bool PACKED, int KS = 1>
 int launch_gemm_unit(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                      int K, int M, hipStream_t stream) {
@@ -1780,10 +1584,8 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
     cfg = wgs >= cu_count() ? 24 : (K > kUnit * kGroup ? 30 : 25);
   }
   switch (cfg) {
-    // measurement alternatives: the earlier double-buffered kernel (0), the
-    // tile kernel (9), other unit-GEMM tile shapes (21-23); 30 is the
-    // two-k-slice unit GEMM
-    case 0: return launch_gemm<2, 2, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
+    // measurement alternatives: the tile kernel (9), other unit-GEMM tile
+    // shapes (21-23); 30 is the two-k-slice unit GEMM
     case 9: return launch_tile<2, 4, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
     case 21: return launch_gemm_unit<1, 4, 8, PACKED>(W, S, X, Y, N, K, M, stream);
     case 22: return launch_gemm_unit<1, 4, 4, PACKED>(W, S, X, Y, N, K, M, stream);
