@@ -1060,23 +1060,20 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
     // the unit's activations, rows clamped to the last valid one
     if (it > 0) __syncthreads();  // previous unit's readers are done
     {
+      // thread tid stages block b = tid % 128 of rows tid / 128 + q * RS
+      constexpr int RS = NT / (kUnit * 16);
+      static_assert(NT % (kUnit * 16) == 0, "a thread keeps one block column");
+      const int b = tid & (kUnit * 16 - 1);
+      const int r0 = tid / (kUnit * 16);
+      const uint16_t* xcol = X + static_cast<size_t>(m0) * K + min(g0 * kGroup + 8 * b, K - 8);
       u32x4_t v[BPT];
 #pragma unroll
-      for (int q = 0; q < BPT; ++q) {
-        const int e = tid + q * NT;
-        const int mm = e / (kUnit * 16);
-        const int b = e - mm * (kUnit * 16);
-        const int kk = min(g0 * kGroup + 8 * b, K - 8);
+      for (int q = 0; q < BPT; ++q)
         v[q] = *reinterpret_cast<const u32x4_t*>(
-            X + static_cast<size_t>(m0 + min(mm, mrows - 1)) * K + kk);
-      }
+            xcol + static_cast<size_t>(min(r0 + q * RS, mrows - 1)) * K);
+      u32x4_t* xdst = xs + r0 * PB + b;
 #pragma unroll
-      for (int q = 0; q < BPT; ++q) {
-        const int e = tid + q * NT;
-        const int mm = e / (kUnit * 16);
-        const int b = e - mm * (kUnit * 16);
-        xs[mm * PB + b] = pair_order(v[q]);
-      }
+      for (int q = 0; q < BPT; ++q) xdst[q * RS * PB] = pair_order(v[q]);
     }
     __syncthreads();
     // offset table of the unit: chains (group, column tile) split over waves
@@ -1591,6 +1588,7 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
     case 22: return launch_gemm_unit<1, 4, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     case 23: return launch_gemm_unit<2, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     case 24: return launch_gemm_unit<1, 2, 8, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 27: return launch_gemm_unit<2, 4, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     case 30: return launch_gemm_unit<1, 2, 4, PACKED, 2>(W, S, X, Y, N, K, M, stream);
     default: return launch_gemm_unit<1, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
   }
