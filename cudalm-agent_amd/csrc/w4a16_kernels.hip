@@ -265,10 +265,10 @@ __device__ __forceinline__ void stage_activations(u32x4_t* xs, int pitch,
 }
 
 // ---------------------------------------------------------------------------
-// Stream kernel: M <= 16, all of x resident in LDS, waves stream 16-row
-// weight tiles (grid-stride) in units of up to 8 groups, prefetching the
-// next unit while the current one is multiplied. NR = accumulator rows per
-// lane that can hold outputs (1 when M == 1, else 4).
+// Stream kernels: M <= 32 (one or two 16-row column tiles, CT), all of x
+// resident in LDS; waves stream 16-row weight tiles (grid-stride), fetching
+// the next piece while the current one is multiplied. NR = accumulator rows
+// per lane that can hold outputs (1 when M == 1, else 4).
 // ---------------------------------------------------------------------------
 
 constexpr int kStreamWaves = 4;
@@ -595,8 +595,10 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
   const int i = lane & 15, a = lane >> 4;
   const int H = (G + HG - 1) / HG;  // pieces per tile
   // Workgroups [0, pwg) are persistent and stride over tiles [0, t_static);
-  // the rest take one tile per wave of [t_static, ntiles) and are dispatched
-  // as persistent workgroups retire.
+  // the rest take one tile per wave of [t_static, ntiles). Most of those are
+  // resident from the start (the CUs hold more workgroups than the
+  // persistent ones) and add loads in flight during the start-up ramp; the
+  // others are placed as workgroups retire.
   const bool persistent = static_cast<int>(blockIdx.x) < pwg;
   const int ntiles = persistent ? t_static : P.tile_end[P.count - 1];
   const int stride = persistent ? pwg * WV : ntiles;
@@ -1400,12 +1402,10 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   const int cap = cu_count() * per_cu;
   const int pwg = want < cap ? want : cap;
   int t_static = ntiles, grid = pwg;
-  // Dispatcher-balanced tail: waves of a static grid finish up to ~4 us
-  // apart on the LM head (XCDs stream at different rates), and for the last
-  // microseconds too few loads are in flight. Handing the last 15% of the
-  // tiles to workgroups that the dispatcher places as persistent ones retire
-  // evens that out: LM head 27.5 -> 25.6 us at M = 1, 30.1 -> 29.7 us at
-  // M = 8; at M >= 16 the tail workgroups' larger x staging makes it slower.
+  // Tail workgroups: the last 15% of the tiles go to one-tile-per-wave
+  // workgroups beyond the persistent grid (LM head 27.5 -> 25.6 us at M = 1,
+  // 30.1 -> 29.7 us at M = 8 in graph replay; at M >= 16 their larger x
+  // staging makes it slower).
   const int tail_pm = M <= 8 ? stream_tail_permille() : 0;
   const int tail = static_cast<int>(static_cast<long long>(ntiles) * tail_pm / 1000);
   if (tail > 0 && ntiles - tail > pwg * WV) {
