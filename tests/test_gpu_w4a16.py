@@ -192,7 +192,8 @@ def test_prefill_chunks(w4, orc, dev, N, K, M):
         assert np.array_equal(Y[b], run(w4, w, s, x[b:b + 1], N, K, 1)[0]), b
 
 
-@pytest.mark.parametrize("N,K", [(37, 384), (1023, 1152), (129, 128), (300, 2176)])
+@pytest.mark.parametrize("N,K", [(37, 384), (1023, 1152), (129, 128), (300, 2176), (1, 128),
+                                 (17, 4096)])
 @pytest.mark.parametrize("M", [33, 70, 129])
 def test_prefill_ragged(w4, orc, dev, N, K, M):
     # the prefill GEMM's partial paths: a last 8-group unit that is short
