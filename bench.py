@@ -350,10 +350,11 @@ def main():
     # ---------------- census: 186 projections + LM head per decode step ----------------
     if not args.no_census:
         calls = census_calls()
-        cw = {}
+        cw, cf = {}, {}
         for li, name, Nc, Kc in calls:
             w, s = synth_weights(torch, Nc, Kc, 0xC0DA0000 + 16 * li + len(name), dev)
             cw[(li, name)] = w4.repack(w, s, Nc, Kc)
+            cf[(li, name)] = (w, s)
         census = {}
         for Mc in (1, 8, 32):
             xs = {Kc: synth_act(torch, Mc, Kc, 0xAC70 + Kc + Mc, dev) for Kc in (1024, 2048, 3584)}
@@ -390,8 +391,28 @@ def main():
                     "GBps": round(tot_bytes / t / 1e9, 1),
                     "frac_hbm_peak": round(tot_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
                 }
+            if Mc == 1:
+                # the drop-in case: the reference's 187 call sites unchanged,
+                # file-layout weights (no repack), one launch per projection
+                fl = [(cf[(li, nm)][0].data_ptr(), cf[(li, nm)][1].data_ptr(),
+                       xs[Kc].data_ptr(), ys[(li, nm)].data_ptr(), Nc, Kc) for li, nm, Nc, Kc in calls]
+
+                def traversal_file(fl=fl):
+                    for wp_, sp_, xx, yy, nn, kk in fl:
+                        lib.cudalm_w4a16_gemv_bf16(wp_, sp_, xx, yy, nn, kk, 1, sraw)
+                    lib.cudalm_w4a16_gemv_bf16(ws[0].data_ptr(), ss[0].data_ptr(), xh.data_ptr(),
+                                               yh.data_ptr(), N, K, 1, sraw)
+
+                t = graph_time(torch, traversal_file, 10, stream)
+                census["M1_file_layout"] = {
+                    "us_per_decode_step": round(t * 1e6, 2),
+                    "launches": len(fl) + 1,
+                    "bytes": tot_bytes,
+                    "GBps": round(tot_bytes / t / 1e9, 1),
+                    "frac_hbm_peak": round(tot_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                }
         extra["census"] = census
-        del cw
+        del cw, cf
 
     # ---------------- prefill chunk GEMM, M = 512 ----------------
     if not args.no_prefill:
