@@ -365,7 +365,11 @@ __device__ __forceinline__ void stream_load_t(StreamUnit& u, const ProjTable& P,
 // One group of one 16-row weight tile against CT 16-row activation tiles:
 // the offset chain comes from the workgroup's table (corr_g), the weight
 // chain seeds from it, and the epilogue applies this lane's row scale.
-template <int NR, int CT, class Act = ActBf16>
+// IOFF: the offset chain is computed here from the group's activation
+// fragments (same operands as the workgroup table, so the same bits)
+// instead of being read from the LDS table; launches whose waves take at
+// most one tile use it to skip the table and its barrier.
+template <int NR, int CT, class Act = ActBf16, bool IOFF = false>
 __device__ __forceinline__ void stream_group(f32x4_t (&acc)[CT], const u32x4_t* const (&xrow)[CT],
                                              int g, u32x4_t w, const float* corr_g, float s,
                                              int a) {
@@ -374,11 +378,16 @@ __device__ __forceinline__ void stream_group(f32x4_t (&acc)[CT], const u32x4_t* 
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     load_group_x(xa[ct], xrow[ct] + g * 16, a);
-    if constexpr (NR == 1) {
-      t[ct] = f32x4_t{corr_g[ct * 16 + 4 * a], 0.0f, 0.0f, 0.0f};
+    f32x4_t c;
+    if constexpr (IOFF) {
+      c = group_offset_t<Act>(xa[ct]);
+    } else if constexpr (NR == 1) {
+      c = f32x4_t{corr_g[ct * 16 + 4 * a], 0.0f, 0.0f, 0.0f};
     } else {
-      t[ct] = *reinterpret_cast<const f32x4_t*>(corr_g + ct * 16 + 4 * a);
+      c = *reinterpret_cast<const f32x4_t*>(corr_g + ct * 16 + 4 * a);
     }
+    // the kernels seed rows 1..3 of a lane with 0 when only row 0 is stored
+    t[ct] = NR == 1 ? f32x4_t{c[0], 0.0f, 0.0f, 0.0f} : c;
   }
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
@@ -399,7 +408,7 @@ __device__ __forceinline__ void stream_group(f32x4_t (&acc)[CT], const u32x4_t* 
 // so it produces the same bits as the kernels that walk units serially.
 
 // One unit (up to 8 groups) of one weight tile into `part`.
-template <int NR, int CT, class Act = ActBf16>
+template <int NR, int CT, class Act = ActBf16, bool IOFF = false>
 __device__ __forceinline__ void stream_unit(f32x4_t (&part)[CT], const StreamUnit& cu,
                                             const u32x4_t* const (&xrow)[CT], const float* corr,
                                             int g0, int gn, int a) {
@@ -407,13 +416,13 @@ __device__ __forceinline__ void stream_unit(f32x4_t (&part)[CT], const StreamUni
     // full unit: straight-line, so independent group chains interleave
 #pragma unroll
     for (int gg = 0; gg < kUnit; ++gg)
-      stream_group<NR, CT, Act>(part, xrow, g0 + gg, cu.w[gg], corr + (g0 + gg) * 16 * CT,
+      stream_group<NR, CT, Act, IOFF>(part, xrow, g0 + gg, cu.w[gg], corr + (g0 + gg) * 16 * CT,
                                 unit_scale(cu.s, gg), a);
   } else {
 #pragma unroll
     for (int gg = 0; gg < kUnit; ++gg)
       if (gg < gn)
-        stream_group<NR, CT, Act>(part, xrow, g0 + gg, cu.w[gg], corr + (g0 + gg) * 16 * CT,
+        stream_group<NR, CT, Act, IOFF>(part, xrow, g0 + gg, cu.w[gg], corr + (g0 + gg) * 16 * CT,
                                   unit_scale(cu.s, gg), a);
   }
 }
@@ -441,7 +450,7 @@ __device__ __forceinline__ void store_tile(const ProjTable& P, int t, const f32x
 // order), then the -1.5 * sum_k x table per (group, row), which is the same
 // for every weight tile (waves split the groups). Returns the LDS offset
 // table; xrow[ct] is this lane's activation row of column tile ct.
-template <int CT, class Act = ActBf16>
+template <int CT, class Act = ActBf16, bool IOFF = false>
 __device__ __forceinline__ float* stream_prologue(u32x4_t* xs, const u32x4_t* (&xrow)[CT],
                                                   const uint16_t* __restrict__ X, int K, int M,
                                                   int wave, int i, int a, const StageBatch& sb0) {
@@ -453,17 +462,19 @@ __device__ __forceinline__ float* stream_prologue(u32x4_t* xs, const u32x4_t* (&
   __syncthreads();
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) xrow[ct] = xs + min(ct * 16 + i, M - 1) * pitch;
-  const int nw = static_cast<int>(blockDim.x >> 6);
-  for (int g = wave; g < G; g += nw) {
+  if constexpr (!IOFF) {
+    const int nw = static_cast<int>(blockDim.x >> 6);
+    for (int g = wave; g < G; g += nw) {
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      u32x4_t xa[4];
-      load_group_x(xa, xrow[ct] + g * 16, a);
-      const f32x4_t c = group_offset_t<Act>(xa);
-      if (i == 0) *reinterpret_cast<f32x4_t*>(corr + (g * CT + ct) * 16 + 4 * a) = c;
+      for (int ct = 0; ct < CT; ++ct) {
+        u32x4_t xa[4];
+        load_group_x(xa, xrow[ct] + g * 16, a);
+        const f32x4_t c = group_offset_t<Act>(xa);
+        if (i == 0) *reinterpret_cast<f32x4_t*>(corr + (g * CT + ct) * 16 + 4 * a) = c;
+      }
     }
+    __syncthreads();
   }
-  __syncthreads();
   return corr;
 }
 
@@ -592,20 +603,20 @@ __device__ __forceinline__ void stream_load_piece(StreamPiece<HG>& h, TileAddr a
   }
 }
 
-template <int HG, int NR, int CT, class Act, bool FULL>
+template <int HG, int NR, int CT, class Act, bool FULL, bool IOFF = false>
 __device__ __forceinline__ void stream_piece(f32x4_t (&part)[CT], const StreamPiece<HG>& h,
                                              const u32x4_t* const (&xrow)[CT], const float* corr,
                                              int g0, int gn, int a) {
 #pragma unroll
   for (int gg = 0; gg < HG; ++gg) {
     if (FULL || gg < gn)
-      stream_group<NR, CT, Act>(part, xrow, g0 + gg, h.w[gg], corr + (g0 + gg) * 16 * CT,
+      stream_group<NR, CT, Act, IOFF>(part, xrow, g0 + gg, h.w[gg], corr + (g0 + gg) * 16 * CT,
                                 half_bits_to_f32((h.s[gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu), a);
   }
 }
 
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, int HG = 4, bool FULL = true,
-          int WV = kStreamWaves>
+          int WV = kStreamWaves, bool IOFF = false>
 __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
     const ProjTable P, const uint16_t* __restrict__ X, int K, int M, int pwg, int t_static) {
   extern __shared__ u32x4_t xs[];
@@ -633,7 +644,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
   TileAddr acur = tile_addr<PACKED>(P, K, G, min(t, ntiles - 1), lane);
   stream_load_piece<HG, PACKED, SVEC, FULL>(cur, acur, G, 0);
   const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a, sb0);
+  const float* corr = stream_prologue<CT, Act, IOFF>(xs, xrow, X, K, M, wave, i, a, sb0);
   if (!active) return;
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -654,7 +665,8 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
     // branching around the loads
     stream_load_piece<HG, PACKED, SVEC, FULL>(nxt, anx, G, (has_next ? nh : h) * HG);
     const int g0 = h * HG;
-    stream_piece<HG, NR, CT, Layout<Act, PACKED>, FULL>(part, cur, xrow, corr, g0, min(HG, G - g0), a);
+    stream_piece<HG, NR, CT, Layout<Act, PACKED>, FULL, IOFF>(part, cur, xrow, corr, g0,
+                                                             min(HG, G - g0), a);
     // an 8-group unit ends after its last piece or at the tile's last piece
     if ((h % PPU) == PPU - 1 || h == H - 1) {
 #pragma unroll
@@ -708,7 +720,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
     stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t0 + sl / U, ntiles - 1), (sl % U) * kUnit, lane);
   }
   const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a, sb0);
+  const float* corr = stream_prologue<CT, Act, true>(xs, xrow, X, K, M, wave, i, a, sb0);
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int sl = wave; sl < nslots; sl += kStreamWaves) {
@@ -719,7 +731,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
     const int g0 = (sl % U) * kUnit;
-    stream_unit<NR, CT, Layout<Act, PACKED>>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
+    stream_unit<NR, CT, Layout<Act, PACKED>, true>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) slots[(sl * CT + ct) * 64 + lane] = part[ct];
   }
@@ -812,7 +824,8 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
   slot_load(cur, min(wave, nslots - 1));
   const u32x4_t* xrow[CT];
   const float* corr =
-      stream_prologue<CT>(xs, xrow, X + static_cast<size_t>(m0) * K, K, mrows, wave, i, a, sb0);
+      stream_prologue<CT, ActBf16, true>(xs, xrow, X + static_cast<size_t>(m0) * K, K, mrows, wave, i,
+                                          a, sb0);
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int sl = wave; sl < nslots; sl += kStreamWaves) {
@@ -821,7 +834,8 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
     const int g0 = (sl % U) * kUnit;
-    stream_unit<NR, CT, Layout<ActBf16, PACKED>>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
+    stream_unit<NR, CT, Layout<ActBf16, PACKED>, true>(part, cur, xrow, corr, g0, min(kUnit, G - g0),
+                                                      a);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) slots[(sl * CT + ct) * 64 + lane] = part[ct];
   }
@@ -1433,10 +1447,18 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
     t_static = ntiles - tail;
     grid = pwg + (tail + WV - 1) / WV;
   }
-  auto kern = mode == 2 ? (G % 2 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, true, WV>
-                                      : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, false, WV>)
-                        : (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV>
-                                      : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV>);
+  // Waves with at most one tile compute their offset chains inline and
+  // skip the workgroup's offset table and its barrier (3584x1024 M=1:
+  // 4.30 -> 4.10 us); waves that stream many tiles share the table (inline
+  // chains cost the LM head 0.9 us at M = 1 and 3.6 us at M = 8).
+  const bool ioff = t_static == ntiles && ntiles <= pwg * WV;
+  auto kern =
+      mode == 2 ? (G % 2 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, true, WV>
+                              : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, false, WV>)
+      : ioff    ? (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, true>
+                              : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, true>)
+                : (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV>
+                              : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV>);
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M, pwg, t_static);
   return launch_status();
