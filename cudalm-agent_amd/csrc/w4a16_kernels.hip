@@ -370,11 +370,9 @@ __device__ __forceinline__ void stream_load_t(StreamUnit& u, const ProjTable& P,
 // instead of being read from the LDS table; launches whose waves take at
 // most one tile use it to skip the table and its barrier.
 template <int NR, int CT, class Act = ActBf16, bool IOFF = false>
-__device__ __forceinline__ void stream_group(f32x4_t (&acc)[CT], const u32x4_t* const (&xrow)[CT],
-                                             int g, u32x4_t w, const float* corr_g, float s,
-                                             int a) {
+__device__ __forceinline__ void group_tmp(f32x4_t (&t)[CT], const u32x4_t* const (&xrow)[CT],
+                                          int g, u32x4_t w, const float* corr_g, int a) {
   u32x4_t xa[CT][4];
-  f32x4_t t[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     load_group_x(xa[ct], xrow[ct] + g * 16, a);
@@ -395,6 +393,14 @@ __device__ __forceinline__ void stream_group(f32x4_t (&acc)[CT], const u32x4_t* 
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) t[ct] = Act::mma(xa[ct][d], B, t[ct]);
   }
+}
+
+template <int NR, int CT, class Act = ActBf16, bool IOFF = false>
+__device__ __forceinline__ void stream_group(f32x4_t (&acc)[CT], const u32x4_t* const (&xrow)[CT],
+                                             int g, u32x4_t w, const float* corr_g, float s,
+                                             int a) {
+  f32x4_t t[CT];
+  group_tmp<NR, CT, Act, IOFF>(t, xrow, g, w, corr_g, a);
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -548,7 +554,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
 template <int HG>
 struct StreamPiece {
   u32x4_t w[HG];
-  uint32_t s[HG / 2];  // fp16 scales of the HG groups for this lane's weight row
+  uint32_t s[(HG + 1) / 2];  // fp16 scales of the HG groups for this lane's weight row
 };
 
 // Lane addresses of one tile: its weight bytes and its fp16 scales at group
@@ -576,7 +582,7 @@ __device__ __forceinline__ TileAddr tile_addr(const ProjTable& P, int K, int G, 
 // FULL: G is a multiple of HG, so no group index needs clamping.
 template <int HG, bool PACKED, bool SVEC, bool FULL>
 __device__ __forceinline__ void stream_load_piece(StreamPiece<HG>& h, TileAddr ad, int G, int g0) {
-  static_assert(HG == 2 || HG == 4, "piece of 2 or 4 groups");
+  static_assert(HG == 1 || HG == 2 || HG == 4, "piece of 1, 2 or 4 groups");
   constexpr int kStep = PACKED ? 1024 : 64;  // bytes between groups of one lane
   const uint8_t* wp = ad.w + static_cast<size_t>(g0) * kStep;
 #pragma unroll
@@ -590,6 +596,8 @@ __device__ __forceinline__ void stream_load_piece(StreamPiece<HG>& h, TileAddr a
       const uint2 sv = *reinterpret_cast<const uint2*>(ad.s + 2 * g0);
       h.s[0] = sv.x;
       h.s[1] = sv.y;
+    } else if constexpr (HG == 1) {
+      h.s[0] = *reinterpret_cast<const uint16_t*>(ad.s + 2 * g0);
     } else {
       h.s[0] = *reinterpret_cast<const uint32_t*>(ad.s + 2 * g0);
     }
@@ -600,6 +608,7 @@ __device__ __forceinline__ void stream_load_piece(StreamPiece<HG>& h, TileAddr a
     for (int gg = 0; gg < HG; ++gg) v[gg] = srow[min(g0 + gg, G - 1)];
 #pragma unroll
     for (int q = 0; q < HG / 2; ++q) h.s[q] = v[2 * q] | (v[2 * q + 1] << 16);
+    if constexpr (HG == 1) h.s[0] = v[0];
   }
 }
 
@@ -742,6 +751,106 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
     for (int ct = 0; ct < CT; ++ct) {
       total[ct] = zero;
       for (int u = 0; u < U; ++u) total[ct] = total[ct] + slots[((wave * U + u) * CT + ct) * 64 + lane];
+    }
+    store_tile<NR, CT, Act>(P, t0 + wave, total, M, i, a);
+  }
+}
+
+// Piece split kernel: the split kernel with pieces of HG groups per wave,
+// so a unit's groups are multiplied on PPU = 8/HG waves side by side. The
+// wave holding a unit's first piece runs its fma chain from 0; the waves
+// holding the later pieces park each group's tmp and scale, and the
+// reducing wave continues the unit's chain over them in group order before
+// the unit sum: the same fma sequence as a serial walk, so the same bits.
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV>
+__global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
+    const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
+  extern __shared__ u32x4_t xs[];
+  constexpr int PPU = kUnit / HG;
+  const int G = K >> 7;
+  const int pitch = (K >> 3) + 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int i = lane & 15, a = lane >> 4;
+  const int ntiles = P.ntiles;
+  const int U = (G + kUnit - 1) / kUnit;
+  const int H = (G + HG - 1) / HG;  // pieces of a tile that hold groups
+  const int SP = U * PPU;           // piece slots of a tile
+  const int TPR = SP >= WV ? 1 : WV / SP;
+  const int nslots = TPR * SP;
+  const int t0 = blockIdx.x * TPR;
+  // after x: heads [TPR*U][CT][64] f32x4, then the later pieces' tmps
+  // [TPR*U][PPU-1][HG][CT][64] f32x4, then their scales [TPR*U][PPU-1][HG][16]
+  f32x4_t* heads = reinterpret_cast<f32x4_t*>(xs + M * pitch);
+  f32x4_t* tmps = heads + TPR * U * CT * 64;
+  float* scs = reinterpret_cast<float*>(tmps + TPR * U * (PPU - 1) * HG * CT * 64);
+
+  StageBatch sb0;
+  stage_load(sb0, X, K, 0, M, 0, K, 0);
+  StreamPiece<HG> cur;
+  auto load_slot = [&](int sl) {
+    const int tt = min(t0 + sl / SP, ntiles - 1);
+    const int h = min(sl % SP, H - 1);
+    stream_load_piece<HG, PACKED, SVEC, false>(cur, tile_addr<PACKED>(P, K, G, tt, lane), G, h * HG);
+  };
+  load_slot(min(wave, nslots - 1));
+  const u32x4_t* xrow[CT];
+  const float* corr = stream_prologue<CT, Act, true>(xs, xrow, X, K, M, wave, i, a, sb0);
+
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int sl = wave; sl < nslots; sl += WV) {
+    if (sl != wave) load_slot(sl);
+    const int tl = sl / SP, h = sl % SP;
+    const int u = h / PPU, pp = h % PPU;
+    const int g0 = h * HG;
+    if (pp == 0) {
+      f32x4_t part[CT];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
+      stream_piece<HG, NR, CT, Layout<Act, PACKED>, false, true>(part, cur, xrow, corr, g0,
+                                                                  min(HG, G - g0), a);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) heads[((tl * U + u) * CT + ct) * 64 + lane] = part[ct];
+    } else if (g0 < G) {
+      const int base = ((tl * U + u) * (PPU - 1) + pp - 1) * HG;
+#pragma unroll
+      for (int gg = 0; gg < HG; ++gg) {
+        if (g0 + gg < G) {
+          f32x4_t t[CT];
+          group_tmp<NR, CT, Layout<Act, PACKED>, true>(t, xrow, g0 + gg, cur.w[gg], corr, a);
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) tmps[((base + gg) * CT + ct) * 64 + lane] = t[ct];
+          if (a == 0)
+            scs[(base + gg) * 16 + i] =
+                half_bits_to_f32((cur.s[gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (wave < TPR && t0 + wave < ntiles) {
+    f32x4_t total[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
+    for (int u = 0; u < U; ++u) {
+      f32x4_t p[CT];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) p[ct] = heads[((wave * U + u) * CT + ct) * 64 + lane];
+      for (int pp = 1; pp < PPU; ++pp) {
+        const int base = ((wave * U + u) * (PPU - 1) + pp - 1) * HG;
+        const int g0 = (u * PPU + pp) * HG;
+        for (int gg = 0; gg < HG && g0 + gg < G; ++gg) {
+          const float sc = scs[(base + gg) * 16 + i];
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) {
+            const f32x4_t t = tmps[((base + gg) * CT + ct) * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) p[ct][r] = __builtin_fmaf(sc, t[r], p[ct][r]);
+          }
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) total[ct] = total[ct] + p[ct];
     }
     store_tile<NR, CT, Act>(P, t0 + wave, total, M, i, a);
   }
@@ -1464,8 +1573,83 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   return launch_status();
 }
 
+// Piece split plan: HG groups per piece, WV waves per workgroup; hg = 0
+// when the unit split or the stream kernel serves the launch. Measured in
+// graph replay over 64 distinct weight sets (us, M = 1 / 8 / 32; the stream
+// or unit split kernel first): 3584x1024 4.08/4.64/7.73 -> 3.56/4.03/5.75
+// with one group per wave on 8 waves; 6144x1024 4.16/4.68/7.76 -> 3.88/
+// 4.28/6.67 with pieces of 2; 1024x2048 4.39/5.36/10.22 -> 4.06/4.87/8.27;
+// 1024x3584 M = 8 6.49 -> 6.00. Eight waves per tile win while the tiles
+// fit one per CU; beyond that pieces of 2 (four waves per tile) win up to
+// the tile counts below, and the persistent stream kernel wins past them.
+// 1024x3584 at M = 1 keeps the unit split (4.52 vs 4.59 us).
+struct SplitPlan {
+  int hg, wv;
+};
+
+size_t split_piece_lds_bytes(int K, int M, SplitPlan p) {
+  const int CT = M > 16 ? 2 : 1;
+  const int PPU = kUnit / p.hg;
+  const int U = (K / kGroup + kUnit - 1) / kUnit;
+  const int SP = U * PPU;
+  const int tpr = SP >= p.wv ? 1 : p.wv / SP;
+  return static_cast<size_t>(M) * (K / 8 + 1) * 16 +
+         static_cast<size_t>(tpr) * U * CT * 64 * 16 * (1 + (PPU - 1) * p.hg) +
+         static_cast<size_t>(tpr) * U * (PPU - 1) * p.hg * 16 * 4;
+}
+
+SplitPlan split_piece_plan(int ntiles, int K, int M) {
+  const int U = (K / kGroup + kUnit - 1) / kUnit;
+  const int cus = cu_count();
+  SplitPlan p = {0, 0};
+  if (M > 32) return p;
+  if (ntiles <= cus && (U == 1 || U == 2 || (U == 4 && M > 1)))
+    p = {U, 8};
+  else if (U == 1 && ntiles <= (M == 1 ? 4 * cus : M <= 16 ? 2 * cus : 4 * cus))
+    p = {2, M == 1 ? 4 : M <= 16 ? 8 : 16};
+  if (p.hg != 0 && split_piece_lds_bytes(K, M, p) > kLdsMax) p = {0, 0};
+  return p;
+}
+
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV>
+int launch_split_piece_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
+  constexpr int PPU = kUnit / HG;
+  const int U = (K / kGroup + kUnit - 1) / kUnit;
+  const int SP = U * PPU;
+  const int tpr = SP >= WV ? 1 : WV / SP;
+  const size_t lds = split_piece_lds_bytes(K, M, SplitPlan{HG, WV});
+  const int grid = (P.ntiles + tpr - 1) / tpr;
+  auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, Act, HG, WV>;
+  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M);
+  return launch_status();
+}
+
+// The plans split_piece_plan can return for this accumulator shape.
+template <bool PACKED, int NR, bool SVEC, int CT, class Act>
+int launch_split_piece(const ProjTable& P, const uint16_t* X, int K, int M, SplitPlan p,
+                       hipStream_t stream) {
+  if (p.hg == 1 && p.wv == 8)
+    return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 1, 8>(P, X, K, M, stream);
+  if (p.hg == 2 && p.wv == 8)
+    return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 8>(P, X, K, M, stream);
+  if constexpr (NR == 1) {
+    if (p.hg == 2 && p.wv == 4)
+      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 4>(P, X, K, M, stream);
+  } else if constexpr (CT == 1) {
+    if (p.hg == 4 && p.wv == 8)
+      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 4, 8>(P, X, K, M, stream);
+  } else {
+    if (p.hg == 2 && p.wv == 16)
+      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 16>(P, X, K, M, stream);
+  }
+  return CUDALM_W4A16_EVARIANT;
+}
+
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
+  const SplitPlan plan = split_piece_plan(P.ntiles, K, M);
+  if (plan.hg != 0) return launch_split_piece<PACKED, NR, SVEC, CT, Act>(P, X, K, M, plan, stream);
   const size_t lds = split_lds_bytes(K, M);
   const int ntiles = P.ntiles;
   const int tpr = split_tiles_per_round(K);
@@ -1525,7 +1709,8 @@ int launch_swiglu(const ProjTable& P, const uint16_t* X, int K, int M, hipStream
 // idle and each tile has several units; otherwise tile-serial streaming.
 bool prefer_split(const ProjTable& P, int K, int M) {
   const int U = (K / kGroup + kUnit - 1) / kUnit;
-  return U >= 2 && split_fits(K, M) && P.ntiles < 2 * cu_count();
+  return split_piece_plan(P.ntiles, K, M).hg != 0 ||
+         (U >= 2 && split_fits(K, M) && P.ntiles < 2 * cu_count());
 }
 
 template <bool PACKED, bool SPLIT, class Act = ActBf16>
@@ -1677,7 +1862,8 @@ int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y
       if (!stream_fits(K, M)) return CUDALM_W4A16_EVARIANT;
       return launch_stream_any<PACKED, false>(single_table(W, S, Y, N), X, K, M, stream);
     case CUDALM_W4A16_VARIANT_SPLIT:
-      if (!split_fits(K, M)) return CUDALM_W4A16_EVARIANT;
+      if (!split_fits(K, M) && split_piece_plan((N + kTileRows - 1) / kTileRows, K, M).hg == 0)
+        return CUDALM_W4A16_EVARIANT;
       return launch_stream_any<PACKED, true>(single_table(W, S, Y, N), X, K, M, stream);
     case CUDALM_W4A16_VARIANT_TILE16:
       return launch_tile<1, 1, 4, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
