@@ -756,106 +756,6 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
   }
 }
 
-// Piece split kernel: the split kernel with pieces of HG groups per wave,
-// so a unit's groups are multiplied on PPU = 8/HG waves side by side. The
-// wave holding a unit's first piece runs its fma chain from 0; the waves
-// holding the later pieces park each group's tmp and scale, and the
-// reducing wave continues the unit's chain over them in group order before
-// the unit sum: the same fma sequence as a serial walk, so the same bits.
-template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV>
-__global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
-    const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
-  extern __shared__ u32x4_t xs[];
-  constexpr int PPU = kUnit / HG;
-  const int G = K >> 7;
-  const int pitch = (K >> 3) + 1;
-  const int lane = threadIdx.x & 63;
-  const int wave = wave_id();
-  const int i = lane & 15, a = lane >> 4;
-  const int ntiles = P.ntiles;
-  const int U = (G + kUnit - 1) / kUnit;
-  const int H = (G + HG - 1) / HG;  // pieces of a tile that hold groups
-  const int SP = U * PPU;           // piece slots of a tile
-  const int TPR = SP >= WV ? 1 : WV / SP;
-  const int nslots = TPR * SP;
-  const int t0 = blockIdx.x * TPR;
-  // after x: heads [TPR*U][CT][64] f32x4, then the later pieces' tmps
-  // [TPR*U][PPU-1][HG][CT][64] f32x4, then their scales [TPR*U][PPU-1][HG][16]
-  f32x4_t* heads = reinterpret_cast<f32x4_t*>(xs + M * pitch);
-  f32x4_t* tmps = heads + TPR * U * CT * 64;
-  float* scs = reinterpret_cast<float*>(tmps + TPR * U * (PPU - 1) * HG * CT * 64);
-
-  StageBatch sb0;
-  stage_load(sb0, X, K, 0, M, 0, K, 0);
-  StreamPiece<HG> cur;
-  auto load_slot = [&](int sl) {
-    const int tt = min(t0 + sl / SP, ntiles - 1);
-    const int h = min(sl % SP, H - 1);
-    stream_load_piece<HG, PACKED, SVEC, false>(cur, tile_addr<PACKED>(P, K, G, tt, lane), G, h * HG);
-  };
-  load_slot(min(wave, nslots - 1));
-  const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT, Act, true>(xs, xrow, X, K, M, wave, i, a, sb0);
-
-  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int sl = wave; sl < nslots; sl += WV) {
-    if (sl != wave) load_slot(sl);
-    const int tl = sl / SP, h = sl % SP;
-    const int u = h / PPU, pp = h % PPU;
-    const int g0 = h * HG;
-    if (pp == 0) {
-      f32x4_t part[CT];
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
-      stream_piece<HG, NR, CT, Layout<Act, PACKED>, false, true>(part, cur, xrow, corr, g0,
-                                                                  min(HG, G - g0), a);
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) heads[((tl * U + u) * CT + ct) * 64 + lane] = part[ct];
-    } else if (g0 < G) {
-      const int base = ((tl * U + u) * (PPU - 1) + pp - 1) * HG;
-#pragma unroll
-      for (int gg = 0; gg < HG; ++gg) {
-        if (g0 + gg < G) {
-          f32x4_t t[CT];
-          group_tmp<NR, CT, Layout<Act, PACKED>, true>(t, xrow, g0 + gg, cur.w[gg], corr, a);
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct) tmps[((base + gg) * CT + ct) * 64 + lane] = t[ct];
-          if (a == 0)
-            scs[(base + gg) * 16 + i] =
-                half_bits_to_f32((cur.s[gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
-        }
-      }
-    }
-  }
-  __syncthreads();
-  if (wave < TPR && t0 + wave < ntiles) {
-    f32x4_t total[CT];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
-    for (int u = 0; u < U; ++u) {
-      f32x4_t p[CT];
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) p[ct] = heads[((wave * U + u) * CT + ct) * 64 + lane];
-      for (int pp = 1; pp < PPU; ++pp) {
-        const int base = ((wave * U + u) * (PPU - 1) + pp - 1) * HG;
-        const int g0 = (u * PPU + pp) * HG;
-        for (int gg = 0; gg < HG && g0 + gg < G; ++gg) {
-          const float sc = scs[(base + gg) * 16 + i];
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct) {
-            const f32x4_t t = tmps[((base + gg) * CT + ct) * 64 + lane];
-#pragma unroll
-            for (int r = 0; r < NR; ++r) p[ct][r] = __builtin_fmaf(sc, t[r], p[ct][r]);
-          }
-        }
-      }
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) total[ct] = total[ct] + p[ct];
-    }
-    store_tile<NR, CT, Act>(P, t0 + wave, total, M, i, a);
-  }
-}
-
 // ---------------------------------------------------------------------------
 // SwiGLU epilogue: the MLP's gate and up projections share x, and the down
 // projection consumes silu(gate) * up (reference: src/runtime/
@@ -964,6 +864,138 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
           P.y[0][static_cast<size_t>(m0 + m) * N + n] = static_cast<uint16_t>(
               silu_mul_bits(f32_to_bf16_rne(16.0f * tg[r]), f32_to_bf16_rne(16.0f * tu[r])));
       }
+    }
+  }
+}
+
+// Piece split kernel: the split kernel with pieces of HG groups per wave,
+// so a unit's groups are multiplied on PPU = 8/HG waves side by side. The
+// wave holding a unit's first piece runs its fma chain from 0; the waves
+// holding the later pieces park each group's tmp and scale, and the
+// reducing wave continues the unit's chain over them in group order before
+// the unit sum: the same fma sequence as a serial walk, so the same bits.
+// NP = 1: the tiles of every projection in P, stored as outputs. NP = 2:
+// SwiGLU; P holds gate then up with equal N, row tile t is gate tile t and
+// up tile nt + t, and the output is silu(gate) * up on the bf16-rounded
+// projections (blockIdx.y walks chunks of mc activation rows).
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, int NP = 1>
+__global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
+    const ProjTable P, const uint16_t* __restrict__ X, int K, int M, int mc) {
+  extern __shared__ u32x4_t xs[];
+  constexpr int PPU = kUnit / HG;
+  const int G = K >> 7;
+  const int pitch = (K >> 3) + 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int i = lane & 15, a = lane >> 4;
+  const int nt = NP == 1 ? P.ntiles : P.tile_end[0];  // row tiles
+  const int U = (G + kUnit - 1) / kUnit;
+  const int H = (G + HG - 1) / HG;  // pieces of a tile that hold groups
+  const int SP = U * PPU;           // piece slots of one projection's tile
+  const int ST = NP * SP;           // piece slots of a row tile
+  const int TPR = ST >= WV ? 1 : WV / ST;
+  const int nslots = TPR * ST;
+  const int t0 = blockIdx.x * TPR;
+  const int m0 = NP == 1 ? 0 : blockIdx.y * mc;
+  const int mrows = NP == 1 ? M : min(mc, M - m0);
+  const uint16_t* Xc = X + static_cast<size_t>(m0) * K;
+  // after x: heads [TPR*NP*U][CT][64] f32x4, then the later pieces' tmps
+  // [TPR*NP*U][PPU-1][HG][CT][64] f32x4, then their scales
+  // [TPR*NP*U][PPU-1][HG][16]
+  f32x4_t* heads = reinterpret_cast<f32x4_t*>(xs + mrows * pitch);
+  f32x4_t* tmps = heads + TPR * NP * U * CT * 64;
+  float* scs = reinterpret_cast<float*>(tmps + TPR * NP * U * (PPU - 1) * HG * CT * 64);
+
+  StageBatch sb0;
+  stage_load(sb0, Xc, K, 0, mrows, 0, K, 0);
+  StreamPiece<HG> cur;
+  // slot sl -> row tile t0 + sl / ST, projection (sl % ST) / SP, piece sl % SP
+  auto load_slot = [&](int sl) {
+    const int tf = min(t0 + sl / ST, nt - 1);
+    const int pj = (sl % ST) / SP;
+    const int h = min(sl % SP, H - 1);
+    stream_load_piece<HG, PACKED, SVEC, false>(cur, tile_addr<PACKED>(P, K, G, pj * nt + tf, lane),
+                                               G, h * HG);
+  };
+  load_slot(min(wave, nslots - 1));
+  const u32x4_t* xrow[CT];
+  const float* corr = stream_prologue<CT, Act, true>(xs, xrow, Xc, K, mrows, wave, i, a, sb0);
+
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int sl = wave; sl < nslots; sl += WV) {
+    if (sl != wave) load_slot(sl);
+    const int tu = sl / SP;  // (row tile, projection) pair, local
+    const int h = sl % SP;
+    const int u = h / PPU, pp = h % PPU;
+    const int g0 = h * HG;
+    if (pp == 0) {
+      f32x4_t part[CT];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
+      stream_piece<HG, NR, CT, Layout<Act, PACKED>, false, true>(part, cur, xrow, corr, g0,
+                                                                  min(HG, G - g0), a);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) heads[((tu * U + u) * CT + ct) * 64 + lane] = part[ct];
+    } else if (g0 < G) {
+      const int base = ((tu * U + u) * (PPU - 1) + pp - 1) * HG;
+#pragma unroll
+      for (int gg = 0; gg < HG; ++gg) {
+        if (g0 + gg < G) {
+          f32x4_t t[CT];
+          group_tmp<NR, CT, Layout<Act, PACKED>, true>(t, xrow, g0 + gg, cur.w[gg], corr, a);
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) tmps[((base + gg) * CT + ct) * 64 + lane] = t[ct];
+          if (a == 0)
+            scs[(base + gg) * 16 + i] =
+                half_bits_to_f32((cur.s[gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (wave < TPR && t0 + wave < nt) {
+    f32x4_t total[NP][CT];
+#pragma unroll
+    for (int pj = 0; pj < NP; ++pj) {
+      const int tu = wave * NP + pj;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) total[pj][ct] = zero;
+      for (int u = 0; u < U; ++u) {
+        f32x4_t p[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) p[ct] = heads[((tu * U + u) * CT + ct) * 64 + lane];
+        for (int pp = 1; pp < PPU; ++pp) {
+          const int base = ((tu * U + u) * (PPU - 1) + pp - 1) * HG;
+          const int g0 = (u * PPU + pp) * HG;
+          for (int gg = 0; gg < HG && g0 + gg < G; ++gg) {
+            const float sc = scs[(base + gg) * 16 + i];
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+              const f32x4_t t = tmps[((base + gg) * CT + ct) * 64 + lane];
+#pragma unroll
+              for (int r = 0; r < NR; ++r) p[ct][r] = __builtin_fmaf(sc, t[r], p[ct][r]);
+            }
+          }
+        }
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) total[pj][ct] = total[pj][ct] + p[ct];
+      }
+    }
+    if constexpr (NP == 1) {
+      store_tile<NR, CT, Act>(P, t0 + wave, total[0], M, i, a);
+    } else {
+      const int N = P.n[0];
+      const int n = (t0 + wave) * kTileRows + i;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const int m = ct * 16 + 4 * a + r;
+          if (m < mrows && n < N)
+            P.y[0][static_cast<size_t>(m0 + m) * N + n] = static_cast<uint16_t>(
+                silu_mul_bits(f32_to_bf16_rne(16.0f * total[0][ct][r]),
+                              f32_to_bf16_rne(16.0f * total[NP - 1][ct][r])));
+        }
     }
   }
 }
@@ -1587,15 +1619,15 @@ struct SplitPlan {
   int hg, wv;
 };
 
-size_t split_piece_lds_bytes(int K, int M, SplitPlan p) {
+size_t split_piece_lds_bytes(int K, int M, SplitPlan p, int NP = 1) {
   const int CT = M > 16 ? 2 : 1;
   const int PPU = kUnit / p.hg;
   const int U = (K / kGroup + kUnit - 1) / kUnit;
-  const int SP = U * PPU;
-  const int tpr = SP >= p.wv ? 1 : p.wv / SP;
+  const int ST = NP * U * PPU;
+  const int tpr = ST >= p.wv ? 1 : p.wv / ST;
   return static_cast<size_t>(M) * (K / 8 + 1) * 16 +
-         static_cast<size_t>(tpr) * U * CT * 64 * 16 * (1 + (PPU - 1) * p.hg) +
-         static_cast<size_t>(tpr) * U * (PPU - 1) * p.hg * 16 * 4;
+         static_cast<size_t>(tpr) * NP * U * CT * 64 * 16 * (1 + (PPU - 1) * p.hg) +
+         static_cast<size_t>(tpr) * NP * U * (PPU - 1) * p.hg * 16 * 4;
 }
 
 SplitPlan split_piece_plan(int ntiles, int K, int M) {
@@ -1621,7 +1653,7 @@ int launch_split_piece_t(const ProjTable& P, const uint16_t* X, int K, int M, hi
   const int grid = (P.ntiles + tpr - 1) / tpr;
   auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, Act, HG, WV>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M, M);
   return launch_status();
 }
 
@@ -1690,10 +1722,58 @@ int swiglu_rows_per_chunk(int K, int M) {
   return mc;
 }
 
+// SwiGLU through the piece split kernel (NP = 2): hg = 0 keeps the unit
+// kernel above. Measured in graph replay over 32 distinct gate/up pairs
+// (us, M = 1 / 8 / 32, unit kernel first): 3584x1024 5.11/5.89/9.58 ->
+// 4.82 (pieces of 4 on 4 waves) / 5.80 (same) / 8.03 (pieces of 2 on 8
+// waves); 9000x1024 6.77/7.67 -> 6.26/7.44, M = 32 unit kernel (12.6 vs
+// 16.1); 1024x2048 M = 1/8 unit kernel (4.86 vs 5.46), M = 32 12.21 ->
+// 10.53 (pieces of 2 on 16 waves).
+SplitPlan swiglu_piece_plan(int nt, int K, int M) {
+  const int U = (K / kGroup + kUnit - 1) / kUnit;
+  const int cus = cu_count();
+  if (U == 1 && M <= 16 && nt <= 4 * cus) return {4, 4};
+  if (U == 1 && nt <= cus) return {2, 8};
+  if (U == 2 && M > 16 && nt <= cus) return {2, 16};
+  return {0, 0};
+}
+
+template <bool PACKED, int NR, bool SVEC, int CT, int HG, int WV>
+int launch_swiglu_piece_t(const ProjTable& P, const uint16_t* X, int K, int M, int mc,
+                          hipStream_t stream) {
+  constexpr int PPU = kUnit / HG;
+  const int U = (K / kGroup + kUnit - 1) / kUnit;
+  const int ST = 2 * U * PPU;
+  const int tpr = ST >= WV ? 1 : WV / ST;
+  const size_t lds = split_piece_lds_bytes(K, mc, SplitPlan{HG, WV}, 2);
+  const int gx = (P.tile_end[0] + tpr - 1) / tpr;
+  const int gy = (M + mc - 1) / mc;
+  if (gy > 65535) return CUDALM_W4A16_ERANGE;
+  auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, ActBf16, HG, WV, 2>;
+  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+  hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(WV * 64), lds, stream, P, X, K, M, mc);
+  return launch_status();
+}
+
 template <bool PACKED>
 int launch_swiglu(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   const int G = K / kGroup;
   const bool svec = !PACKED && G % 8 == 0 && aligned(P.s[0], 16) && aligned(P.s[1], 16);
+  const SplitPlan plan = swiglu_piece_plan(P.tile_end[0], K, M);
+  if (plan.hg != 0) {
+    int mc = M > 16 ? 32 : M;
+    while (mc > 0 && split_piece_lds_bytes(K, mc, plan, 2) > kLdsMax) --mc;
+    // a plan for M > 16 needs 32-row chunks (CT = 2)
+    if (mc > 0 && (M <= 16 || mc > 16)) {
+#define W4A16_SWP(NR, CT, HG, WV)                                                      \
+  (svec ? launch_swiglu_piece_t<PACKED, NR, true, CT, HG, WV>(P, X, K, M, mc, stream) \
+        : launch_swiglu_piece_t<PACKED, NR, false, CT, HG, WV>(P, X, K, M, mc, stream))
+      if (mc > 16) return plan.wv == 16 ? W4A16_SWP(4, 2, 2, 16) : W4A16_SWP(4, 2, 2, 8);
+      if (M == 1) return W4A16_SWP(1, 1, 4, 4);
+      return W4A16_SWP(4, 1, 4, 4);
+#undef W4A16_SWP
+    }
+  }
   const int mc = swiglu_rows_per_chunk(K, M);
   if (mc < 1) return CUDALM_W4A16_ERANGE;
 #define W4A16_SWIGLU(NR, CT)                                                       \

@@ -89,7 +89,8 @@ def three_step(w4, gw, gs, uw, us, x, N, K, M, packed):
     return down(g), down(u), down(y)
 
 
-@pytest.mark.parametrize("N,K", [(3584, 1024), (37, 256), (100, 3584), (16, 1024)])
+@pytest.mark.parametrize("N,K", [(3584, 1024), (37, 256), (100, 3584), (16, 1024), (1000, 2048),
+                                 (5000, 640)])
 @pytest.mark.parametrize("M", [1, 3, 8, 16, 17, 32, 33, 64, 100])
 @pytest.mark.parametrize("packed", [False, True])
 def test_fused_swiglu_equals_three_step(w4, orc, dev, N, K, M, packed):
