@@ -370,12 +370,10 @@ __device__ __forceinline__ void stream_load_t(StreamUnit& u, const ProjTable& P,
 // instead of being read from the LDS table; launches whose waves take at
 // most one tile use it to skip the table and its barrier.
 template <int NR, int CT, class Act = ActBf16, bool IOFF = false>
-__device__ __forceinline__ void group_tmp(f32x4_t (&t)[CT], const u32x4_t* const (&xrow)[CT],
-                                          int g, u32x4_t w, const float* corr_g, int a) {
-  u32x4_t xa[CT][4];
+__device__ __forceinline__ void group_tmp_x(f32x4_t (&t)[CT], const u32x4_t (&xa)[CT][4],
+                                            u32x4_t w, const float* corr_g, int a) {
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    load_group_x(xa[ct], xrow[ct] + g * 16, a);
     f32x4_t c;
     if constexpr (IOFF) {
       c = group_offset_t<Act>(xa[ct]);
@@ -392,6 +390,30 @@ __device__ __forceinline__ void group_tmp(f32x4_t (&t)[CT], const u32x4_t* const
     const u32x4_t B = Act::decode(w[d]);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) t[ct] = Act::mma(xa[ct][d], B, t[ct]);
+  }
+}
+
+template <int NR, int CT, class Act = ActBf16, bool IOFF = false>
+__device__ __forceinline__ void group_tmp(f32x4_t (&t)[CT], const u32x4_t* const (&xrow)[CT],
+                                          int g, u32x4_t w, const float* corr_g, int a) {
+  u32x4_t xa[CT][4];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) load_group_x(xa[ct], xrow[ct] + g * 16, a);
+  group_tmp_x<NR, CT, Act, IOFF>(t, xa, w, corr_g, a);
+}
+
+// A lane's activation fragments of group g straight from global memory, in
+// the pair order the LDS staging writes (row = min(ct * 16 + i, mrows - 1)).
+template <int CT>
+__device__ __forceinline__ void load_group_x_global(u32x4_t (&xa)[CT][4],
+                                                    const uint16_t* __restrict__ X, int K,
+                                                    int mrows, int g, int i, int a) {
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(
+        X + static_cast<size_t>(min(ct * 16 + i, mrows - 1)) * K + g * kGroup + 32 * a);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) xa[ct][d] = pair_order(src[d]);
   }
 }
 
@@ -878,7 +900,8 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
 // SwiGLU; P holds gate then up with equal N, row tile t is gate tile t and
 // up tile nt + t, and the output is silu(gate) * up on the bf16-rounded
 // projections (blockIdx.y walks chunks of mc activation rows).
-template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, int NP = 1>
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, int NP = 1,
+          bool DX = false>
 __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
     const ProjTable P, const uint16_t* __restrict__ X, int K, int M, int mc) {
   extern __shared__ u32x4_t xs[];
@@ -899,27 +922,35 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
   const int m0 = NP == 1 ? 0 : blockIdx.y * mc;
   const int mrows = NP == 1 ? M : min(mc, M - m0);
   const uint16_t* Xc = X + static_cast<size_t>(m0) * K;
-  // after x: heads [TPR*NP*U][CT][64] f32x4, then the later pieces' tmps
-  // [TPR*NP*U][PPU-1][HG][CT][64] f32x4, then their scales
+  // after x (none with DX): heads [TPR*NP*U][CT][64] f32x4, then the later
+  // pieces' tmps [TPR*NP*U][PPU-1][HG][CT][64] f32x4, then their scales
   // [TPR*NP*U][PPU-1][HG][16]
-  f32x4_t* heads = reinterpret_cast<f32x4_t*>(xs + mrows * pitch);
+  f32x4_t* heads = reinterpret_cast<f32x4_t*>(xs + (DX ? 0 : mrows * pitch));
   f32x4_t* tmps = heads + TPR * NP * U * CT * 64;
   float* scs = reinterpret_cast<float*>(tmps + TPR * NP * U * (PPU - 1) * HG * CT * 64);
 
   StageBatch sb0;
-  stage_load(sb0, Xc, K, 0, mrows, 0, K, 0);
+  if constexpr (!DX) stage_load(sb0, Xc, K, 0, mrows, 0, K, 0);
   StreamPiece<HG> cur;
+  // DX: the piece's activation fragments, loaded by the wave itself
+  u32x4_t xg[DX ? HG : 1][CT][4];
   // slot sl -> row tile t0 + sl / ST, projection (sl % ST) / SP, piece sl % SP
   auto load_slot = [&](int sl) {
     const int tf = min(t0 + sl / ST, nt - 1);
     const int pj = (sl % ST) / SP;
     const int h = min(sl % SP, H - 1);
+    if constexpr (DX) {
+#pragma unroll
+      for (int gg = 0; gg < HG; ++gg)
+        load_group_x_global<CT>(xg[DX ? gg : 0], Xc, K, mrows, min(h * HG + gg, G - 1), i, a);
+    }
     stream_load_piece<HG, PACKED, SVEC, false>(cur, tile_addr<PACKED>(P, K, G, pj * nt + tf, lane),
                                                G, h * HG);
   };
   load_slot(min(wave, nslots - 1));
   const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT, Act, true>(xs, xrow, Xc, K, mrows, wave, i, a, sb0);
+  const float* corr = nullptr;
+  if constexpr (!DX) corr = stream_prologue<CT, Act, true>(xs, xrow, Xc, K, mrows, wave, i, a, sb0);
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int sl = wave; sl < nslots; sl += WV) {
@@ -932,8 +963,23 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
       f32x4_t part[CT];
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
-      stream_piece<HG, NR, CT, Layout<Act, PACKED>, false, true>(part, cur, xrow, corr, g0,
-                                                                  min(HG, G - g0), a);
+      if constexpr (DX) {
+#pragma unroll
+        for (int gg = 0; gg < HG; ++gg) {
+          if (gg < G - g0) {
+            f32x4_t t[CT];
+            group_tmp_x<NR, CT, Layout<Act, PACKED>, true>(t, xg[DX ? gg : 0], cur.w[gg], corr, a);
+            const float sc = half_bits_to_f32((cur.s[gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+              for (int r = 0; r < NR; ++r) part[ct][r] = __builtin_fmaf(sc, t[ct][r], part[ct][r]);
+          }
+        }
+      } else {
+        stream_piece<HG, NR, CT, Layout<Act, PACKED>, false, true>(part, cur, xrow, corr, g0,
+                                                                    min(HG, G - g0), a);
+      }
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) heads[((tu * U + u) * CT + ct) * 64 + lane] = part[ct];
     } else if (g0 < G) {
@@ -942,7 +988,10 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
       for (int gg = 0; gg < HG; ++gg) {
         if (g0 + gg < G) {
           f32x4_t t[CT];
-          group_tmp<NR, CT, Layout<Act, PACKED>, true>(t, xrow, g0 + gg, cur.w[gg], corr, a);
+          if constexpr (DX)
+            group_tmp_x<NR, CT, Layout<Act, PACKED>, true>(t, xg[DX ? gg : 0], cur.w[gg], corr, a);
+          else
+            group_tmp<NR, CT, Layout<Act, PACKED>, true>(t, xrow, g0 + gg, cur.w[gg], corr, a);
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct) tmps[((base + gg) * CT + ct) * 64 + lane] = t[ct];
           if (a == 0)
@@ -1270,37 +1319,44 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) part[rb][ct] = zero;
+    // one group: offset-seeded weight chains, then the scale fma into part
+    auto group = [&](int gg) {
+      u32x4_t xa[CT][4];
+      f32x4_t t[RB][CT];
 #pragma unroll
-    for (int gg = 0; gg < kUnit; ++gg) {
-      if (gg < gn) {
-        u32x4_t xa[CT][4];
-        f32x4_t t[RB][CT];
+      for (int ct = 0; ct < CT; ++ct) {
+        load_group_x(xa[ct], xs + (ct * 16 + i) * PB + gg * 16, a);
+        const f32x4_t o = *reinterpret_cast<const f32x4_t*>(corr + (gg * CT + ct) * 16 + 4 * a);
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          load_group_x(xa[ct], xs + (ct * 16 + i) * PB + gg * 16, a);
-          const f32x4_t o = *reinterpret_cast<const f32x4_t*>(corr + (gg * CT + ct) * 16 + 4 * a);
+        for (int rb = 0; rb < RB; ++rb) t[rb][ct] = o;
+      }
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb) t[rb][ct] = o;
-        }
+      for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
+        for (int d = 0; d < 4; ++d) {
+          const u32x4_t B = decode_nibbles<PACKED>(w[rb][gg][d]);
 #pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const u32x4_t B = decode_nibbles<PACKED>(w[rb][gg][d]);
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) t[rb][ct] = mfma16(xa[ct][d], B, t[rb][ct]);
-          }
-        }
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          const float s = half_bits_to_f32((sc[rb][gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              part[rb][ct][r] = __builtin_fmaf(s, t[rb][ct][r], part[rb][ct][r]);
+          for (int ct = 0; ct < CT; ++ct) t[rb][ct] = mfma16(xa[ct][d], B, t[rb][ct]);
         }
       }
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const float s = half_bits_to_f32((sc[rb][gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            part[rb][ct][r] = __builtin_fmaf(s, t[rb][ct][r], part[rb][ct][r]);
+      }
+    };
+    if (gn == kUnit) {
+      // full unit: straight-line, so independent group chains interleave
+#pragma unroll
+      for (int gg = 0; gg < kUnit; ++gg) group(gg);
+    } else {
+#pragma unroll
+      for (int gg = 0; gg < kUnit; ++gg)
+        if (gg < gn) group(gg);
     }
     if constexpr (KS == 1) {
 #pragma unroll
@@ -1615,8 +1671,18 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
 // fit one per CU; beyond that pieces of 2 (four waves per tile) win up to
 // the tile counts below, and the persistent stream kernel wins past them.
 // 1024x3584 at M = 1 keeps the unit split (4.52 vs 4.59 us).
+//
+// dx: each wave loads its pieces' activation fragments straight from global
+// memory into registers, so neither the LDS staging nor its barrier sits in
+// front of the first MFMA (us, M = 1 / 8 / 32, LDS staging -> direct):
+// 512x1024 2.94/3.56/5.35 -> 2.49/3.02/4.57; 3584x1024 3.53/4.03/5.75 ->
+// 3.05/3.53/5.00; 1024x2048 4.07/4.88/8.31 -> 3.68/4.48/7.29; 6144x1024
+// 3.88/4.27 -> 3.52/4.15. Sixteen-wave workgroups of four tiles at M > 16
+// load x four times per CU instead of staging it once: 6144x1024 M = 32
+// 6.68 -> 10.73, so they keep the staging.
 struct SplitPlan {
   int hg, wv;
+  bool dx;
 };
 
 size_t split_piece_lds_bytes(int K, int M, SplitPlan p, int NP = 1) {
@@ -1625,7 +1691,7 @@ size_t split_piece_lds_bytes(int K, int M, SplitPlan p, int NP = 1) {
   const int U = (K / kGroup + kUnit - 1) / kUnit;
   const int ST = NP * U * PPU;
   const int tpr = ST >= p.wv ? 1 : p.wv / ST;
-  return static_cast<size_t>(M) * (K / 8 + 1) * 16 +
+  return (p.dx ? 0 : static_cast<size_t>(M) * (K / 8 + 1) * 16) +
          static_cast<size_t>(tpr) * NP * U * CT * 64 * 16 * (1 + (PPU - 1) * p.hg) +
          static_cast<size_t>(tpr) * NP * U * (PPU - 1) * p.hg * 16 * 4;
 }
@@ -1633,25 +1699,25 @@ size_t split_piece_lds_bytes(int K, int M, SplitPlan p, int NP = 1) {
 SplitPlan split_piece_plan(int ntiles, int K, int M) {
   const int U = (K / kGroup + kUnit - 1) / kUnit;
   const int cus = cu_count();
-  SplitPlan p = {0, 0};
+  SplitPlan p = {0, 0, false};
   if (M > 32) return p;
   if (ntiles <= cus && (U == 1 || U == 2 || (U == 4 && M > 1)))
-    p = {U, 8};
+    p = {U, 8, true};
   else if (U == 1 && ntiles <= (M == 1 ? 4 * cus : M <= 16 ? 2 * cus : 4 * cus))
-    p = {2, M == 1 ? 4 : M <= 16 ? 8 : 16};
-  if (p.hg != 0 && split_piece_lds_bytes(K, M, p) > kLdsMax) p = {0, 0};
+    p = {2, M == 1 ? 4 : M <= 16 ? 8 : 16, M <= 16};
+  if (p.hg != 0 && split_piece_lds_bytes(K, M, p) > kLdsMax) p = {0, 0, false};
   return p;
 }
 
-template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV>
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, bool DX>
 int launch_split_piece_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   constexpr int PPU = kUnit / HG;
   const int U = (K / kGroup + kUnit - 1) / kUnit;
   const int SP = U * PPU;
   const int tpr = SP >= WV ? 1 : WV / SP;
-  const size_t lds = split_piece_lds_bytes(K, M, SplitPlan{HG, WV});
+  const size_t lds = split_piece_lds_bytes(K, M, SplitPlan{HG, WV, DX});
   const int grid = (P.ntiles + tpr - 1) / tpr;
-  auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, Act, HG, WV>;
+  auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, Act, HG, WV, 1, DX>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M, M);
   return launch_status();
@@ -1661,19 +1727,20 @@ int launch_split_piece_t(const ProjTable& P, const uint16_t* X, int K, int M, hi
 template <bool PACKED, int NR, bool SVEC, int CT, class Act>
 int launch_split_piece(const ProjTable& P, const uint16_t* X, int K, int M, SplitPlan p,
                        hipStream_t stream) {
-  if (p.hg == 1 && p.wv == 8)
-    return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 1, 8>(P, X, K, M, stream);
-  if (p.hg == 2 && p.wv == 8)
-    return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 8>(P, X, K, M, stream);
+  if (p.hg == 1 && p.wv == 8 && p.dx)
+    return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 1, 8, true>(P, X, K, M, stream);
+  if (p.hg == 2 && p.wv == 8 && p.dx)
+    return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 8, true>(P, X, K, M, stream);
   if constexpr (NR == 1) {
-    if (p.hg == 2 && p.wv == 4)
-      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 4>(P, X, K, M, stream);
-  } else if constexpr (CT == 1) {
-    if (p.hg == 4 && p.wv == 8)
-      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 4, 8>(P, X, K, M, stream);
+    if (p.hg == 2 && p.wv == 4 && p.dx)
+      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 4, true>(P, X, K, M, stream);
   } else {
-    if (p.hg == 2 && p.wv == 16)
-      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 16>(P, X, K, M, stream);
+    if (p.hg == 4 && p.wv == 8 && p.dx)
+      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 4, 8, true>(P, X, K, M, stream);
+  }
+  if constexpr (CT == 2) {
+    if (p.hg == 2 && p.wv == 16 && !p.dx)
+      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 16, false>(P, X, K, M, stream);
   }
   return CUDALM_W4A16_EVARIANT;
 }
@@ -1729,27 +1796,32 @@ int swiglu_rows_per_chunk(int K, int M) {
 // waves); 9000x1024 6.77/7.67 -> 6.26/7.44, M = 32 unit kernel (12.6 vs
 // 16.1); 1024x2048 M = 1/8 unit kernel (4.86 vs 5.46), M = 32 12.21 ->
 // 10.53 (pieces of 2 on 16 waves).
+//
+// Direct activation loads (dx) pay at M <= 16 while the row tiles fit one
+// per CU: 3584x1024 M = 1/8 4.82/5.81 -> 4.39/5.37 us; at M = 32 (8.0 ->
+// 8.6) and past one row tile per CU (9000x1024 M = 8 7.41 -> 7.83) the LDS
+// staging wins.
 SplitPlan swiglu_piece_plan(int nt, int K, int M) {
   const int U = (K / kGroup + kUnit - 1) / kUnit;
   const int cus = cu_count();
-  if (U == 1 && M <= 16 && nt <= 4 * cus) return {4, 4};
-  if (U == 1 && nt <= cus) return {2, 8};
-  if (U == 2 && M > 16 && nt <= cus) return {2, 16};
-  return {0, 0};
+  if (U == 1 && M <= 16 && nt <= 4 * cus) return {4, 4, nt <= cus};
+  if (U == 1 && nt <= cus) return {2, 8, false};
+  if (U == 2 && M > 16 && nt <= cus) return {2, 16, false};
+  return {0, 0, false};
 }
 
-template <bool PACKED, int NR, bool SVEC, int CT, int HG, int WV>
+template <bool PACKED, int NR, bool SVEC, int CT, int HG, int WV, bool DX>
 int launch_swiglu_piece_t(const ProjTable& P, const uint16_t* X, int K, int M, int mc,
                           hipStream_t stream) {
   constexpr int PPU = kUnit / HG;
   const int U = (K / kGroup + kUnit - 1) / kUnit;
   const int ST = 2 * U * PPU;
   const int tpr = ST >= WV ? 1 : WV / ST;
-  const size_t lds = split_piece_lds_bytes(K, mc, SplitPlan{HG, WV}, 2);
+  const size_t lds = split_piece_lds_bytes(K, mc, SplitPlan{HG, WV, DX}, 2);
   const int gx = (P.tile_end[0] + tpr - 1) / tpr;
   const int gy = (M + mc - 1) / mc;
   if (gy > 65535) return CUDALM_W4A16_ERANGE;
-  auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, ActBf16, HG, WV, 2>;
+  auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, ActBf16, HG, WV, 2, DX>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
   hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(WV * 64), lds, stream, P, X, K, M, mc);
   return launch_status();
@@ -1765,12 +1837,13 @@ int launch_swiglu(const ProjTable& P, const uint16_t* X, int K, int M, hipStream
     while (mc > 0 && split_piece_lds_bytes(K, mc, plan, 2) > kLdsMax) --mc;
     // a plan for M > 16 needs 32-row chunks (CT = 2)
     if (mc > 0 && (M <= 16 || mc > 16)) {
-#define W4A16_SWP(NR, CT, HG, WV)                                                      \
-  (svec ? launch_swiglu_piece_t<PACKED, NR, true, CT, HG, WV>(P, X, K, M, mc, stream) \
-        : launch_swiglu_piece_t<PACKED, NR, false, CT, HG, WV>(P, X, K, M, mc, stream))
-      if (mc > 16) return plan.wv == 16 ? W4A16_SWP(4, 2, 2, 16) : W4A16_SWP(4, 2, 2, 8);
-      if (M == 1) return W4A16_SWP(1, 1, 4, 4);
-      return W4A16_SWP(4, 1, 4, 4);
+#define W4A16_SWP(NR, CT, HG, WV, DX)                                                      \
+  (svec ? launch_swiglu_piece_t<PACKED, NR, true, CT, HG, WV, DX>(P, X, K, M, mc, stream) \
+        : launch_swiglu_piece_t<PACKED, NR, false, CT, HG, WV, DX>(P, X, K, M, mc, stream))
+      if (mc > 16)
+        return plan.wv == 16 ? W4A16_SWP(4, 2, 2, 16, false) : W4A16_SWP(4, 2, 2, 8, false);
+      if (M == 1) return plan.dx ? W4A16_SWP(1, 1, 4, 4, true) : W4A16_SWP(1, 1, 4, 4, false);
+      return plan.dx ? W4A16_SWP(4, 1, 4, 4, true) : W4A16_SWP(4, 1, 4, 4, false);
 #undef W4A16_SWP
     }
   }
