@@ -48,6 +48,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "cudalm_w4a16.h"
 #include "hip_common.h"
 
@@ -1679,7 +1681,10 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
 // 3.05/3.53/5.00; 1024x2048 4.07/4.88/8.31 -> 3.68/4.48/7.29; 6144x1024
 // 3.88/4.27 -> 3.52/4.15. Sixteen-wave workgroups of four tiles at M > 16
 // load x four times per CU instead of staging it once: 6144x1024 M = 32
-// 6.68 -> 10.73, so they keep the staging.
+// 6.68 -> 10.73, so they keep the staging. With direct x, one tile per
+// 4-wave workgroup in pieces of 2 serves 2 <= M <= 16 past one tile per
+// CU: 6144x1024 M = 8 4.28 -> 4.12, 8208x1024 4.86 (stream) -> 4.41,
+// 12288x1024 4.97 (stream) -> 4.87; 16384x1024 stays on the stream kernel.
 struct SplitPlan {
   int hg, wv;
   bool dx;
@@ -1701,10 +1706,21 @@ SplitPlan split_piece_plan(int ntiles, int K, int M) {
   const int cus = cu_count();
   SplitPlan p = {0, 0, false};
   if (M > 32) return p;
+#ifdef CUDALM_EXPLORE
+  if (const char* e = getenv("CUDALM_EXPLORE_PLAN")) {
+    const int v = atoi(e);  // hg, wv, dx as digits: 4081 = {4, 8, dx}
+    if (v > 0) {
+      p = {v / 1000, (v / 10) % 100, (v % 10) != 0};
+      if (split_piece_lds_bytes(K, M, p) > kLdsMax) p = {0, 0, false};
+      return p;
+    }
+    if (v < 0) return p;
+  }
+#endif
   if (ntiles <= cus && (U == 1 || U == 2 || (U == 4 && M > 1)))
     p = {U, 8, true};
-  else if (U == 1 && ntiles <= (M == 1 ? 4 * cus : M <= 16 ? 2 * cus : 4 * cus))
-    p = {2, M == 1 ? 4 : M <= 16 ? 8 : 16, M <= 16};
+  else if (U == 1 && ntiles <= (M <= 16 ? (M == 1 ? 4 : 3) * cus : 4 * cus))
+    p = {2, M <= 16 ? 4 : 16, M <= 16};
   if (p.hg != 0 && split_piece_lds_bytes(K, M, p) > kLdsMax) p = {0, 0, false};
   return p;
 }
@@ -1731,10 +1747,11 @@ int launch_split_piece(const ProjTable& P, const uint16_t* X, int K, int M, Spli
     return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 1, 8, true>(P, X, K, M, stream);
   if (p.hg == 2 && p.wv == 8 && p.dx)
     return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 8, true>(P, X, K, M, stream);
-  if constexpr (NR == 1) {
+  if constexpr (CT == 1) {
     if (p.hg == 2 && p.wv == 4 && p.dx)
       return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 4, true>(P, X, K, M, stream);
-  } else {
+  }
+  if constexpr (NR == 4) {
     if (p.hg == 4 && p.wv == 8 && p.dx)
       return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 4, 8, true>(P, X, K, M, stream);
   }
@@ -1742,6 +1759,17 @@ int launch_split_piece(const ProjTable& P, const uint16_t* X, int K, int M, Spli
     if (p.hg == 2 && p.wv == 16 && !p.dx)
       return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 16, false>(P, X, K, M, stream);
   }
+#ifdef CUDALM_EXPLORE
+  if constexpr (PACKED && std::is_same<Act, ActBf16>::value) {
+#define X_SP(HG, WV)                                                                         \
+  if (p.hg == HG && p.wv == WV)                                                             \
+    return p.dx ? launch_split_piece_t<PACKED, NR, SVEC, CT, Act, HG, WV, true>(P, X, K, M, stream) \
+                : launch_split_piece_t<PACKED, NR, SVEC, CT, Act, HG, WV, false>(P, X, K, M, stream);
+    X_SP(1, 4) X_SP(1, 8) X_SP(1, 16) X_SP(2, 4) X_SP(2, 8) X_SP(2, 16) X_SP(4, 4) X_SP(4, 8)
+    X_SP(4, 16)
+#undef X_SP
+  }
+#endif
   return CUDALM_W4A16_EVARIANT;
 }
 
@@ -1798,13 +1826,22 @@ int swiglu_rows_per_chunk(int K, int M) {
 // 10.53 (pieces of 2 on 16 waves).
 //
 // Direct activation loads (dx) pay at M <= 16 while the row tiles fit one
-// per CU: 3584x1024 M = 1/8 4.82/5.81 -> 4.39/5.37 us; at M = 32 (8.0 ->
-// 8.6) and past one row tile per CU (9000x1024 M = 8 7.41 -> 7.83) the LDS
-// staging wins.
+// per CU, best with pieces of 2 on 8 waves: 3584x1024 M = 1/8 4.82/5.81 ->
+// 4.14/5.33 us, 4096x1024 M = 1 4.40 (pieces of 4, dx) -> 4.12; at M = 32
+// (8.0 -> 8.6) and past one row tile per CU (9000x1024 M = 8 7.41 -> 7.83)
+// the LDS staging wins.
 SplitPlan swiglu_piece_plan(int nt, int K, int M) {
   const int U = (K / kGroup + kUnit - 1) / kUnit;
   const int cus = cu_count();
-  if (U == 1 && M <= 16 && nt <= 4 * cus) return {4, 4, nt <= cus};
+#ifdef CUDALM_EXPLORE
+  if (const char* e = getenv("CUDALM_EXPLORE_SWPLAN")) {
+    const int v = atoi(e);
+    if (v > 0) return {v / 1000, (v / 10) % 100, (v % 10) != 0};
+    if (v < 0) return {0, 0, false};
+  }
+#endif
+  if (U == 1 && M <= 16 && nt <= cus) return {2, 8, true};
+  if (U == 1 && M <= 16 && nt <= 4 * cus) return {4, 4, false};
   if (U == 1 && nt <= cus) return {2, 8, false};
   if (U == 2 && M > 16 && nt <= cus) return {2, 16, false};
   return {0, 0, false};
@@ -1840,10 +1877,21 @@ int launch_swiglu(const ProjTable& P, const uint16_t* X, int K, int M, hipStream
 #define W4A16_SWP(NR, CT, HG, WV, DX)                                                      \
   (svec ? launch_swiglu_piece_t<PACKED, NR, true, CT, HG, WV, DX>(P, X, K, M, mc, stream) \
         : launch_swiglu_piece_t<PACKED, NR, false, CT, HG, WV, DX>(P, X, K, M, mc, stream))
+#ifdef CUDALM_EXPLORE
+      if constexpr (PACKED) {
+#define X_SW(NR, CT, HG, WV) \
+  if (plan.hg == HG && plan.wv == WV) \
+    return plan.dx ? W4A16_SWP(NR, CT, HG, WV, true) : W4A16_SWP(NR, CT, HG, WV, false);
+        if (mc > 16) { X_SW(4, 2, 1, 8) X_SW(4, 2, 1, 16) X_SW(4, 2, 2, 8) X_SW(4, 2, 2, 16) X_SW(4, 2, 4, 4) X_SW(4, 2, 4, 8) }
+        else if (M == 1) { X_SW(1, 1, 1, 8) X_SW(1, 1, 1, 16) X_SW(1, 1, 2, 8) X_SW(1, 1, 2, 4) X_SW(1, 1, 4, 4) X_SW(1, 1, 4, 8) }
+        else { X_SW(4, 1, 1, 8) X_SW(4, 1, 1, 16) X_SW(4, 1, 2, 8) X_SW(4, 1, 2, 4) X_SW(4, 1, 4, 4) X_SW(4, 1, 4, 8) }
+#undef X_SW
+      }
+#endif
       if (mc > 16)
         return plan.wv == 16 ? W4A16_SWP(4, 2, 2, 16, false) : W4A16_SWP(4, 2, 2, 8, false);
-      if (M == 1) return plan.dx ? W4A16_SWP(1, 1, 4, 4, true) : W4A16_SWP(1, 1, 4, 4, false);
-      return plan.dx ? W4A16_SWP(4, 1, 4, 4, true) : W4A16_SWP(4, 1, 4, 4, false);
+      if (M == 1) return plan.dx ? W4A16_SWP(1, 1, 2, 8, true) : W4A16_SWP(1, 1, 4, 4, false);
+      return plan.dx ? W4A16_SWP(4, 1, 2, 8, true) : W4A16_SWP(4, 1, 4, 4, false);
 #undef W4A16_SWP
     }
   }
