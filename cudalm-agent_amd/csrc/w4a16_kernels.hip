@@ -48,8 +48,6 @@
 #include <stdint.h>
 #include <stdlib.h>
 
-#include <type_traits>
-
 #include "cudalm_w4a16.h"
 #include "hip_common.h"
 
@@ -1706,17 +1704,6 @@ SplitPlan split_piece_plan(int ntiles, int K, int M) {
   const int cus = cu_count();
   SplitPlan p = {0, 0, false};
   if (M > 32) return p;
-#ifdef CUDALM_EXPLORE
-  if (const char* e = getenv("CUDALM_EXPLORE_PLAN")) {
-    const int v = atoi(e);  // hg, wv, dx as digits: 4081 = {4, 8, dx}
-    if (v > 0) {
-      p = {v / 1000, (v / 10) % 100, (v % 10) != 0};
-      if (split_piece_lds_bytes(K, M, p) > kLdsMax) p = {0, 0, false};
-      return p;
-    }
-    if (v < 0) return p;
-  }
-#endif
   if (ntiles <= cus && (U == 1 || U == 2 || (U == 4 && M > 1)))
     p = {U, 8, true};
   else if (U == 1 && ntiles <= (M <= 16 ? (M == 1 ? 4 : 3) * cus : 4 * cus))
@@ -1759,17 +1746,6 @@ int launch_split_piece(const ProjTable& P, const uint16_t* X, int K, int M, Spli
     if (p.hg == 2 && p.wv == 16 && !p.dx)
       return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 16, false>(P, X, K, M, stream);
   }
-#ifdef CUDALM_EXPLORE
-  if constexpr (PACKED && std::is_same<Act, ActBf16>::value) {
-#define X_SP(HG, WV)                                                                         \
-  if (p.hg == HG && p.wv == WV)                                                             \
-    return p.dx ? launch_split_piece_t<PACKED, NR, SVEC, CT, Act, HG, WV, true>(P, X, K, M, stream) \
-                : launch_split_piece_t<PACKED, NR, SVEC, CT, Act, HG, WV, false>(P, X, K, M, stream);
-    X_SP(1, 4) X_SP(1, 8) X_SP(1, 16) X_SP(2, 4) X_SP(2, 8) X_SP(2, 16) X_SP(4, 4) X_SP(4, 8)
-    X_SP(4, 16)
-#undef X_SP
-  }
-#endif
   return CUDALM_W4A16_EVARIANT;
 }
 
@@ -1833,13 +1809,6 @@ int swiglu_rows_per_chunk(int K, int M) {
 SplitPlan swiglu_piece_plan(int nt, int K, int M) {
   const int U = (K / kGroup + kUnit - 1) / kUnit;
   const int cus = cu_count();
-#ifdef CUDALM_EXPLORE
-  if (const char* e = getenv("CUDALM_EXPLORE_SWPLAN")) {
-    const int v = atoi(e);
-    if (v > 0) return {v / 1000, (v / 10) % 100, (v % 10) != 0};
-    if (v < 0) return {0, 0, false};
-  }
-#endif
   if (U == 1 && M <= 16 && nt <= cus) return {2, 8, true};
   if (U == 1 && M <= 16 && nt <= 4 * cus) return {4, 4, false};
   if (U == 1 && nt <= cus) return {2, 8, false};
@@ -1877,17 +1846,6 @@ int launch_swiglu(const ProjTable& P, const uint16_t* X, int K, int M, hipStream
 #define W4A16_SWP(NR, CT, HG, WV, DX)                                                      \
   (svec ? launch_swiglu_piece_t<PACKED, NR, true, CT, HG, WV, DX>(P, X, K, M, mc, stream) \
         : launch_swiglu_piece_t<PACKED, NR, false, CT, HG, WV, DX>(P, X, K, M, mc, stream))
-#ifdef CUDALM_EXPLORE
-      if constexpr (PACKED) {
-#define X_SW(NR, CT, HG, WV) \
-  if (plan.hg == HG && plan.wv == WV) \
-    return plan.dx ? W4A16_SWP(NR, CT, HG, WV, true) : W4A16_SWP(NR, CT, HG, WV, false);
-        if (mc > 16) { X_SW(4, 2, 1, 8) X_SW(4, 2, 1, 16) X_SW(4, 2, 2, 8) X_SW(4, 2, 2, 16) X_SW(4, 2, 4, 4) X_SW(4, 2, 4, 8) }
-        else if (M == 1) { X_SW(1, 1, 1, 8) X_SW(1, 1, 1, 16) X_SW(1, 1, 2, 8) X_SW(1, 1, 2, 4) X_SW(1, 1, 4, 4) X_SW(1, 1, 4, 8) }
-        else { X_SW(4, 1, 1, 8) X_SW(4, 1, 1, 16) X_SW(4, 1, 2, 8) X_SW(4, 1, 2, 4) X_SW(4, 1, 4, 4) X_SW(4, 1, 4, 8) }
-#undef X_SW
-      }
-#endif
       if (mc > 16)
         return plan.wv == 16 ? W4A16_SWP(4, 2, 2, 16, false) : W4A16_SWP(4, 2, 2, 8, false);
       if (M == 1) return plan.dx ? W4A16_SWP(1, 1, 2, 8, true) : W4A16_SWP(1, 1, 4, 4, false);
