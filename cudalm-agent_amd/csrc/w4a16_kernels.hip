@@ -1993,11 +1993,19 @@ int launch_bytewise(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint
 }
 
 
+// The piece split with activations in registers needs no LDS for x, so it
+// also serves 17 <= M <= 32 when x does not fit the LDS (1024x3584 at
+// M = 32: one launch instead of two 16-row passes).
+bool piece_direct(int ntiles, int K, int M) {
+  const SplitPlan p = split_piece_plan(ntiles, K, M);
+  return p.hg != 0 && p.dx;
+}
+
 template <bool PACKED>
 int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N, int K,
              int M, int variant, hipStream_t stream) {
   if (variant == CUDALM_W4A16_VARIANT_AUTO) {
-    if (stream_fits(K, M)) {
+    if (stream_fits(K, M) || piece_direct((N + kTileRows - 1) / kTileRows, K, M)) {
       const ProjTable P = single_table(W, S, Y, N);
       return launch_stream<PACKED>(P, X, K, M, stream);
     } else if (M <= 32 && M > 16) {
@@ -2153,7 +2161,8 @@ int cudalm_w4a16_gemv_bf16_multi(const cudalm_w4a16_proj* projs, int count, cons
   if (prepacked && !vec_ok) return CUDALM_W4A16_EALIGN;
   long long tiles = 0;
   for (int j = 0; j < count; ++j) tiles += (projs[j].N + kTileRows - 1) / kTileRows;
-  if (!vec_ok || !stream_fits(K, M) || tiles > (1LL << 30)) {
+  if (!vec_ok || tiles > (1LL << 30) ||
+      (!stream_fits(K, M) && !piece_direct(static_cast<int>(tiles), K, M))) {
     // not one fused launch: one call per projection (same bits)
     for (int j = 0; j < count; ++j) {
       const int rc =
