@@ -1198,7 +1198,7 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
 
 constexpr int kSliceMaxUnits = 4;  // units per k-slice kept as partials (KS > 1)
 
-template <int RB, int CT, int WV, bool PACKED, bool SVEC, int KS = 1>
+template <int RB, int CT, int WV, bool PACKED, bool SVEC, int KS = 1, bool IOFF = false>
 __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
     const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
     const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, int N, int K, int M) {
@@ -1304,14 +1304,18 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
     }
     __syncthreads();
     // offset table of the unit: chains (group, column tile) split over waves
-    for (int c = wave; c < kUnit * CT; c += WV) {
-      const int gg = c / CT, ct = c - gg * CT;
-      u32x4_t xa[4];
-      load_group_x(xa, xs + (ct * 16 + i) * PB + gg * 16, a);
-      const f32x4_t o = group_offset(xa);
-      if (i == 0) *reinterpret_cast<f32x4_t*>(corr + c * 16 + 4 * a) = o;
+    // (IOFF: each wave runs the chains of its own groups inline instead, the
+    // same operands, and the table and its barrier are skipped)
+    if constexpr (!IOFF) {
+      for (int c = wave; c < kUnit * CT; c += WV) {
+        const int gg = c / CT, ct = c - gg * CT;
+        u32x4_t xa[4];
+        load_group_x(xa, xs + (ct * 16 + i) * PB + gg * 16, a);
+        const f32x4_t o = group_offset(xa);
+        if (i == 0) *reinterpret_cast<f32x4_t*>(corr + c * 16 + 4 * a) = o;
+      }
+      __syncthreads();
     }
-    __syncthreads();
     if (!any_ok) continue;
 
     f32x4_t part[RB][CT];
@@ -1326,7 +1330,8 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         load_group_x(xa[ct], xs + (ct * 16 + i) * PB + gg * 16, a);
-        const f32x4_t o = *reinterpret_cast<const f32x4_t*>(corr + (gg * CT + ct) * 16 + 4 * a);
+        const f32x4_t o = IOFF ? group_offset(xa[ct])
+                               : *reinterpret_cast<const f32x4_t*>(corr + (gg * CT + ct) * 16 + 4 * a);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) t[rb][ct] = o;
       }
@@ -1924,7 +1929,7 @@ int launch_tile(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t
   return launch_status();
 }
 
-template <int RB, int CT, int WV, bool PACKED, int KS = 1>
+template <int RB, int CT, int WV, bool PACKED, int KS = 1, bool IOFF = false>
 int launch_gemm_unit(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                      int K, int M, hipStream_t stream) {
   constexpr int TM = CT * 16;
@@ -1937,15 +1942,15 @@ int launch_gemm_unit(const uint8_t* W, const uint16_t* S, const uint16_t* X, uin
     const int U = (G + kUnit - 1) / kUnit;
     if (U > KS * kSliceMaxUnits ||
         static_cast<size_t>(U) * WV * RB * CT * 64 * 16 > KS * xbytes)
-      return launch_gemm_unit<RB, CT, WV, PACKED, 1>(W, S, X, Y, N, K, M, stream);
+      return launch_gemm_unit<RB, CT, WV, PACKED, 1, IOFF>(W, S, X, Y, N, K, M, stream);
   }
   const int ntiles = (N + kTileRows - 1) / kTileRows;
   const int gx = (ntiles + WV * RB - 1) / (WV * RB);
   const int gy = (M + TM - 1) / TM;
   if (gy > 65535) return CUDALM_W4A16_ERANGE;
   const bool svec = !PACKED && G % 8 == 0 && aligned(S, 16);
-  auto kern = svec ? w4a16_gemm_unit_kernel<RB, CT, WV, PACKED, true, KS>
-                   : w4a16_gemm_unit_kernel<RB, CT, WV, PACKED, false, KS>;
+  auto kern = svec ? w4a16_gemm_unit_kernel<RB, CT, WV, PACKED, true, KS, IOFF>
+                   : w4a16_gemm_unit_kernel<RB, CT, WV, PACKED, false, KS, IOFF>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
   hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(WV * KS * 64), lds, stream, W, S, X, Y, N, K, M);
   return launch_status();
@@ -1964,7 +1969,10 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
   if (cfg < 0) {
     // unit GEMM: 128 x 32 workgroup tiles of 8 waves while they fill the
     // CUs, else 64 x 32 tiles of 4 waves, with two k-slices of 4 waves when
-    // K spans several units (1024x3584 at M = 512: 16.7 -> 14.6 us)
+    // K spans several units (1024x3584 at M = 512: 16.7 -> 14.6 us). The
+    // 4-wave tiles run their offset chains inline (512x1024x512 5.8 ->
+    // 5.5 us, 1024x3584x512 14.4 -> 13.8 us); inline chains cost the
+    // 8-wave tiles 0.6 us at 3584x1024x512, so those keep the table.
     const long long wgs = static_cast<long long>((N + 127) / 128) * ((M + 31) / 32);
     cfg = wgs >= cu_count() ? 24 : (K > kUnit * kGroup ? 30 : 25);
   }
@@ -1977,8 +1985,8 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
     case 23: return launch_gemm_unit<2, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
     case 24: return launch_gemm_unit<1, 2, 8, PACKED>(W, S, X, Y, N, K, M, stream);
     case 27: return launch_gemm_unit<2, 4, 4, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 30: return launch_gemm_unit<1, 2, 4, PACKED, 2>(W, S, X, Y, N, K, M, stream);
-    default: return launch_gemm_unit<1, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
+    case 30: return launch_gemm_unit<1, 2, 4, PACKED, 2, true>(W, S, X, Y, N, K, M, stream);
+    default: return launch_gemm_unit<1, 2, 4, PACKED, 1, true>(W, S, X, Y, N, K, M, stream);
   }
 }
 
