@@ -1967,14 +1967,16 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
                    int M, hipStream_t stream) {
   int cfg = gemm_config();
   if (cfg < 0) {
-    // unit GEMM: 128 x 32 workgroup tiles of 8 waves while they fill the
-    // CUs, else 64 x 32 tiles of 4 waves, with two k-slices of 4 waves when
+    // unit GEMM: 128 x 32 workgroup tiles of 8 waves while they fill most
+    // of the CUs, else 64 x 32 tiles of 4 waves, with two k-slices of 4 waves when
     // K spans several units (1024x3584 at M = 512: 16.7 -> 14.6 us). The
     // 4-wave tiles run their offset chains inline (512x1024x512 5.8 ->
     // 5.5 us, 1024x3584x512 14.4 -> 13.8 us); inline chains cost the
     // 8-wave tiles 0.6 us at 3584x1024x512, so those keep the table.
     const long long wgs = static_cast<long long>((N + 127) / 128) * ((M + 31) / 32);
-    cfg = wgs >= cu_count() ? 24 : (K > kUnit * kGroup ? 30 : 25);
+    // (crossover measured between 128 and 168 workgroups of 128 x 32:
+    // 2048x1024x256 5.7 vs 6.9 us, 3584x1024x192 7.4 vs 6.9 us)
+    cfg = 5 * wgs >= 3LL * cu_count() ? 24 : (K > kUnit * kGroup ? 30 : 25);
   }
   switch (cfg) {
     // measurement alternatives: the tile kernel (9), other unit-GEMM tile
