@@ -316,6 +316,23 @@ __device__ __forceinline__ ProjView proj_view(const ProjTable& P, int t) {
   return v;
 }
 
+// A single projection with ProjTable's field names (count 1): 40 bytes of
+// kernel arguments instead of 264, for the launches that carry one
+// projection.
+struct ProjOne {
+  const uint8_t* w[1];
+  const uint16_t* s[1];
+  uint16_t* y[1];
+  int n[1];
+  int tile_end[1];
+  int count;
+  int ntiles;
+};
+
+__device__ __forceinline__ ProjView proj_view(const ProjOne& P, int) {
+  return {P.w[0], P.s[0], P.y[0], P.n[0], 0};
+}
+
 struct StreamUnit {
   u32x4_t w[kUnit];
   u32x4_t s;  // fp16 scales of the unit's 8 groups for this lane's weight row
@@ -355,8 +372,8 @@ __device__ __forceinline__ void stream_load(StreamUnit& u, const uint8_t* __rest
   }
 }
 
-template <bool PACKED, bool SVEC>
-__device__ __forceinline__ void stream_load_t(StreamUnit& u, const ProjTable& P, int K, int G,
+template <bool PACKED, bool SVEC, class PT>
+__device__ __forceinline__ void stream_load_t(StreamUnit& u, const PT& P, int K, int G,
                                               int t, int g0, int lane) {
   const ProjView v = proj_view(P, t);
   stream_load<PACKED, SVEC>(u, v.w, v.s, v.n, K, G, t - v.begin, g0, lane);
@@ -455,8 +472,8 @@ __device__ __forceinline__ void stream_unit(f32x4_t (&part)[CT], const StreamUni
   }
 }
 
-template <int NR, int CT, class Act = ActBf16>
-__device__ __forceinline__ void store_tile(const ProjTable& P, int t, const f32x4_t (&total)[CT],
+template <int NR, int CT, class Act = ActBf16, class PT = ProjTable>
+__device__ __forceinline__ void store_tile(const PT& P, int t, const f32x4_t (&total)[CT],
                                            int M, int i, int a) {
   const ProjView v = proj_view(P, t);
   const int Nj = v.n;
@@ -586,8 +603,8 @@ struct TileAddr {
   const uint8_t* s;
 };
 
-template <bool PACKED>
-__device__ __forceinline__ TileAddr tile_addr(const ProjTable& P, int K, int G, int t, int lane) {
+template <bool PACKED, class PT>
+__device__ __forceinline__ TileAddr tile_addr(const PT& P, int K, int G, int t, int lane) {
   const ProjView v = proj_view(P, t);
   const int rt = t - v.begin;
   const int i = lane & 15, a = lane >> 4;
@@ -724,9 +741,9 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
 // partials of those tiles side by side, park them in LDS, and the unit
 // partials of each tile are summed in unit order. Same bits as the stream
 // kernel; shorter latency when tiles alone cannot fill the machine.
-template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
+template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, class PT = ProjTable>
 __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
-    const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
+    const PT P, const uint16_t* __restrict__ X, int K, int M) {
   extern __shared__ u32x4_t xs[];
   const int G = K >> 7;
   const int pitch = (K >> 3) + 1;
@@ -774,7 +791,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
       total[ct] = zero;
       for (int u = 0; u < U; ++u) total[ct] = total[ct] + slots[((wave * U + u) * CT + ct) * 64 + lane];
     }
-    store_tile<NR, CT, Act>(P, t0 + wave, total, M, i, a);
+    store_tile<NR, CT, Act, PT>(P, t0 + wave, total, M, i, a);
   }
 }
 
@@ -901,9 +918,9 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
 // up tile nt + t, and the output is silu(gate) * up on the bf16-rounded
 // projections (blockIdx.y walks chunks of mc activation rows).
 template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, int NP = 1,
-          bool DX = false>
+          bool DX = false, class PT = ProjTable>
 __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
-    const ProjTable P, const uint16_t* __restrict__ X, int K, int M, int mc) {
+    const PT P, const uint16_t* __restrict__ X, int K, int M, int mc) {
   extern __shared__ u32x4_t xs[];
   constexpr int PPU = kUnit / HG;
   const int G = K >> 7;
@@ -1031,7 +1048,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
       }
     }
     if constexpr (NP == 1) {
-      store_tile<NR, CT, Act>(P, t0 + wave, total[0], M, i, a);
+      store_tile<NR, CT, Act, PT>(P, t0 + wave, total[0], M, i, a);
     } else {
       const int N = P.n[0];
       const int n = (t0 + wave) * kTileRows + i;
@@ -1693,6 +1710,13 @@ struct SplitPlan {
   bool dx;
 };
 
+// Single-projection launches pass a 40-byte argument struct
+// (CUDALM_W4A16_SPLIT_ONE, measurement only: 0 = the full table).
+int split_one_table() {
+  static const int v = env_setting("CUDALM_W4A16_SPLIT_ONE", 1, 0, 1);
+  return v;
+}
+
 size_t split_piece_lds_bytes(int K, int M, SplitPlan p, int NP = 1) {
   const int CT = M > 16 ? 2 : 1;
   const int PPU = kUnit / p.hg;
@@ -1717,39 +1741,39 @@ SplitPlan split_piece_plan(int ntiles, int K, int M) {
   return p;
 }
 
-template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, bool DX>
-int launch_split_piece_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, bool DX, class PT>
+int launch_split_piece_t(const PT& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   constexpr int PPU = kUnit / HG;
   const int U = (K / kGroup + kUnit - 1) / kUnit;
   const int SP = U * PPU;
   const int tpr = SP >= WV ? 1 : WV / SP;
   const size_t lds = split_piece_lds_bytes(K, M, SplitPlan{HG, WV, DX});
   const int grid = (P.ntiles + tpr - 1) / tpr;
-  auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, Act, HG, WV, 1, DX>;
+  auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, Act, HG, WV, 1, DX, PT>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M, M);
   return launch_status();
 }
 
 // The plans split_piece_plan can return for this accumulator shape.
-template <bool PACKED, int NR, bool SVEC, int CT, class Act>
-int launch_split_piece(const ProjTable& P, const uint16_t* X, int K, int M, SplitPlan p,
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, class PT>
+int launch_split_piece(const PT& P, const uint16_t* X, int K, int M, SplitPlan p,
                        hipStream_t stream) {
   if (p.hg == 1 && p.wv == 8 && p.dx)
-    return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 1, 8, true>(P, X, K, M, stream);
+    return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 1, 8, true, PT>(P, X, K, M, stream);
   if (p.hg == 2 && p.wv == 8 && p.dx)
-    return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 8, true>(P, X, K, M, stream);
+    return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 8, true, PT>(P, X, K, M, stream);
   if constexpr (CT == 1) {
     if (p.hg == 2 && p.wv == 4 && p.dx)
-      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 4, true>(P, X, K, M, stream);
+      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 4, true, PT>(P, X, K, M, stream);
   }
   if constexpr (NR == 4) {
     if (p.hg == 4 && p.wv == 8 && p.dx)
-      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 4, 8, true>(P, X, K, M, stream);
+      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 4, 8, true, PT>(P, X, K, M, stream);
   }
   if constexpr (CT == 2) {
     if (p.hg == 2 && p.wv == 16 && !p.dx)
-      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 16, false>(P, X, K, M, stream);
+      return launch_split_piece_t<PACKED, NR, SVEC, CT, Act, 2, 16, false, PT>(P, X, K, M, stream);
   }
   return CUDALM_W4A16_EVARIANT;
 }
@@ -1757,11 +1781,24 @@ int launch_split_piece(const ProjTable& P, const uint16_t* X, int K, int M, Spli
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   const SplitPlan plan = split_piece_plan(P.ntiles, K, M);
-  if (plan.hg != 0) return launch_split_piece<PACKED, NR, SVEC, CT, Act>(P, X, K, M, plan, stream);
+  if (plan.hg != 0) {
+    if (P.count == 1 && split_one_table()) {
+      const ProjOne one = {{P.w[0]}, {P.s[0]}, {P.y[0]}, {P.n[0]}, {P.tile_end[0]}, 1, P.ntiles};
+      return launch_split_piece<PACKED, NR, SVEC, CT, Act>(one, X, K, M, plan, stream);
+    }
+    return launch_split_piece<PACKED, NR, SVEC, CT, Act>(P, X, K, M, plan, stream);
+  }
   const size_t lds = split_lds_bytes(K, M);
   const int ntiles = P.ntiles;
   const int tpr = split_tiles_per_round(K);
   const int grid = (ntiles + tpr - 1) / tpr;
+  if (P.count == 1 && split_one_table()) {
+    const ProjOne one = {{P.w[0]}, {P.s[0]}, {P.y[0]}, {P.n[0]}, {P.tile_end[0]}, 1, P.ntiles};
+    auto kern = w4a16_split_kernel<PACKED, NR, SVEC, CT, Act, ProjOne>;
+    if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kStreamWaves * 64), lds, stream, one, X, K, M);
+    return launch_status();
+  }
   auto kern = w4a16_split_kernel<PACKED, NR, SVEC, CT, Act>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kStreamWaves * 64), lds, stream, P, X, K, M);
