@@ -48,6 +48,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "cudalm_w4a16.h"
 #include "hip_common.h"
 
@@ -664,9 +666,9 @@ __device__ __forceinline__ void stream_piece(f32x4_t (&part)[CT], const StreamPi
 }
 
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, int HG = 4, bool FULL = true,
-          int WV = kStreamWaves, bool IOFF = false>
+          int WV = kStreamWaves, bool IOFF = false, class PT = ProjTable>
 __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
-    const ProjTable P, const uint16_t* __restrict__ X, int K, int M, int pwg, int t_static) {
+    const PT P, const uint16_t* __restrict__ X, int K, int M, int pwg, int t_static) {
   extern __shared__ u32x4_t xs[];
   constexpr int PPU = kUnit / HG;  // pieces per 8-group unit
   const int G = K >> 7;
@@ -724,7 +726,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
       }
     }
     if (h == H - 1) {
-      store_tile<NR, CT, Act>(P, t, total, M, i, a);
+      store_tile<NR, CT, Act, PT>(P, t, total, M, i, a);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
     }
@@ -1621,6 +1623,14 @@ int stream_tail_permille() {
   return v;
 }
 
+// Single-projection launches pass a 40-byte argument struct (ProjOne)
+// instead of the 264-byte table (CUDALM_W4A16_PROJ_ONE, measurement only:
+// 0 = the full table).
+int proj_one_enabled() {
+  static const int v = env_setting("CUDALM_W4A16_PROJ_ONE", 1, 0, 1);
+  return v;
+}
+
 // Workgroups per CU of the 8-wave stream kernel (two column tiles).
 int stream_occupancy_wide() {
   static const int occ = env_setting("CUDALM_W4A16_STREAM_WIDE_WGS_PER_CU", 2, 1, 8);
@@ -1671,16 +1681,26 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   // 4.30 -> 4.10 us); waves that stream many tiles share the table (inline
   // chains cost the LM head 0.9 us at M = 1 and 3.6 us at M = 8).
   const bool ioff = t_static == ntiles && ntiles <= pwg * WV;
-  auto kern =
-      mode == 2 ? (G % 2 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, true, WV>
-                              : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, false, WV>)
-      : ioff    ? (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, true>
-                              : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, true>)
-                : (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV>
-                              : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV>);
-  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M, pwg, t_static);
-  return launch_status();
+  auto go = [&](const auto& T) {
+    using PT = std::decay_t<decltype(T)>;
+    auto kern =
+        mode == 2
+            ? (G % 2 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, true, WV, false, PT>
+                          : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, false, WV, false, PT>)
+        : ioff
+            ? (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, true, PT>
+                          : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, true, PT>)
+            : (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, false, PT>
+                          : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, false, PT>);
+    if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, T, X, K, M, pwg, t_static);
+    return launch_status();
+  };
+  if (P.count == 1 && proj_one_enabled()) {
+    const ProjOne one = {{P.w[0]}, {P.s[0]}, {P.y[0]}, {P.n[0]}, {P.tile_end[0]}, 1, P.ntiles};
+    return go(one);
+  }
+  return go(P);
 }
 
 // Piece split plan: HG groups per piece, WV waves per workgroup; hg = 0
@@ -1710,12 +1730,6 @@ struct SplitPlan {
   bool dx;
 };
 
-// Single-projection launches pass a 40-byte argument struct
-// (CUDALM_W4A16_SPLIT_ONE, measurement only: 0 = the full table).
-int split_one_table() {
-  static const int v = env_setting("CUDALM_W4A16_SPLIT_ONE", 1, 0, 1);
-  return v;
-}
 
 size_t split_piece_lds_bytes(int K, int M, SplitPlan p, int NP = 1) {
   const int CT = M > 16 ? 2 : 1;
@@ -1782,7 +1796,7 @@ template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   const SplitPlan plan = split_piece_plan(P.ntiles, K, M);
   if (plan.hg != 0) {
-    if (P.count == 1 && split_one_table()) {
+    if (P.count == 1 && proj_one_enabled()) {
       const ProjOne one = {{P.w[0]}, {P.s[0]}, {P.y[0]}, {P.n[0]}, {P.tile_end[0]}, 1, P.ntiles};
       return launch_split_piece<PACKED, NR, SVEC, CT, Act>(one, X, K, M, plan, stream);
     }
@@ -1792,7 +1806,7 @@ int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStrea
   const int ntiles = P.ntiles;
   const int tpr = split_tiles_per_round(K);
   const int grid = (ntiles + tpr - 1) / tpr;
-  if (P.count == 1 && split_one_table()) {
+  if (P.count == 1 && proj_one_enabled()) {
     const ProjOne one = {{P.w[0]}, {P.s[0]}, {P.y[0]}, {P.n[0]}, {P.tile_end[0]}, 1, P.ntiles};
     auto kern = w4a16_split_kernel<PACKED, NR, SVEC, CT, Act, ProjOne>;
     if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
