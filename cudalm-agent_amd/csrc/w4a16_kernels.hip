@@ -279,21 +279,30 @@ constexpr int kMaxProj = CUDALM_W4A16_MAX_PROJ;
 // Projections that share one activation matrix, streamed by one launch.
 // Tiles are numbered globally; projection j owns tiles
 // [tile_end[j-1], tile_end[j]).
-struct ProjTable {
-  const uint8_t* w[kMaxProj];
-  const uint16_t* s[kMaxProj];
-  uint16_t* y[kMaxProj];
-  int n[kMaxProj];
-  int tile_end[kMaxProj];
+// Up to NMAX projections sharing x; tiles are numbered globally in
+// projection order. Launches pass the smallest table that holds their
+// projections: kernel arguments and the lookup below grow with NMAX (the
+// 264-byte table of 8 cost the LM head 0.26 us over the 40-byte one).
+template <int NMAX>
+struct ProjTab {
+  const uint8_t* w[NMAX];
+  const uint16_t* s[NMAX];
+  uint16_t* y[NMAX];
+  int n[NMAX];
+  int tile_end[NMAX];
   int count;
   int ntiles;  // tile_end[count - 1]
 };
+using ProjTable = ProjTab<kMaxProj>;
+using ProjOne = ProjTab<1>;
+using ProjFour = ProjTab<4>;
 
 // The projection that owns tile t. Every field is read at a constant
 // offset and chosen with scalar selects, so the kernel-argument loads are
 // independent of each other (a data-dependent index would chain three
 // kernel-argument round trips ahead of the first weight load; that cost
 // 0.35-0.6 us per small launch).
+
 struct ProjView {
   const uint8_t* w;
   const uint16_t* s;
@@ -302,37 +311,41 @@ struct ProjView {
   int begin;  // first global tile of the projection
 };
 
-__device__ __forceinline__ ProjView proj_view(const ProjTable& P, int t) {
+template <int NMAX>
+__device__ __forceinline__ ProjView proj_view(const ProjTab<NMAX>& P, int t) {
   ProjView v = {P.w[0], P.s[0], P.y[0], P.n[0], 0};
-  if (P.count == 1) return v;
+  if constexpr (NMAX == 1) {
+    return v;
+  } else {
+    if (P.count == 1) return v;
 #pragma unroll
-  for (int k = 1; k < kMaxProj; ++k) {
-    if (k < P.count && t >= P.tile_end[k - 1]) {
-      v.w = P.w[k];
-      v.s = P.s[k];
-      v.y = P.y[k];
-      v.n = P.n[k];
-      v.begin = P.tile_end[k - 1];
+    for (int k = 1; k < NMAX; ++k) {
+      if (k < P.count && t >= P.tile_end[k - 1]) {
+        v.w = P.w[k];
+        v.s = P.s[k];
+        v.y = P.y[k];
+        v.n = P.n[k];
+        v.begin = P.tile_end[k - 1];
+      }
     }
+    return v;
   }
-  return v;
 }
 
-// A single projection with ProjTable's field names (count 1): 40 bytes of
-// kernel arguments instead of 264, for the launches that carry one
-// projection.
-struct ProjOne {
-  const uint8_t* w[1];
-  const uint16_t* s[1];
-  uint16_t* y[1];
-  int n[1];
-  int tile_end[1];
-  int count;
-  int ntiles;
-};
-
-__device__ __forceinline__ ProjView proj_view(const ProjOne& P, int) {
-  return {P.w[0], P.s[0], P.y[0], P.n[0], 0};
+// A copy of the first `count` projections of P in a smaller table.
+template <int NMAX>
+ProjTab<NMAX> shrink_table(const ProjTable& P) {
+  ProjTab<NMAX> T = {};
+  for (int j = 0; j < P.count && j < NMAX; ++j) {
+    T.w[j] = P.w[j];
+    T.s[j] = P.s[j];
+    T.y[j] = P.y[j];
+    T.n[j] = P.n[j];
+    T.tile_end[j] = P.tile_end[j];
+  }
+  T.count = P.count;
+  T.ntiles = P.ntiles;
+  return T;
 }
 
 struct StreamUnit {
@@ -1697,7 +1710,7 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
     return launch_status();
   };
   if (P.count == 1 && proj_one_enabled()) {
-    const ProjOne one = {{P.w[0]}, {P.s[0]}, {P.y[0]}, {P.n[0]}, {P.tile_end[0]}, 1, P.ntiles};
+    const ProjOne one = shrink_table<1>(P);
     return go(one);
   }
   return go(P);
@@ -1797,8 +1810,15 @@ int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStrea
   const SplitPlan plan = split_piece_plan(P.ntiles, K, M);
   if (plan.hg != 0) {
     if (P.count == 1 && proj_one_enabled()) {
-      const ProjOne one = {{P.w[0]}, {P.s[0]}, {P.y[0]}, {P.n[0]}, {P.tile_end[0]}, 1, P.ntiles};
+      const ProjOne one = shrink_table<1>(P);
       return launch_split_piece<PACKED, NR, SVEC, CT, Act>(one, X, K, M, plan, stream);
+    }
+    if constexpr (std::is_same<Act, ActBf16>::value) {
+      // the fused projection groups (qkv/z/b/a, q/k/v, gate/up) have <= 4
+      if (P.count <= 4 && proj_one_enabled()) {
+        const ProjFour four = shrink_table<4>(P);
+        return launch_split_piece<PACKED, NR, SVEC, CT, Act>(four, X, K, M, plan, stream);
+      }
     }
     return launch_split_piece<PACKED, NR, SVEC, CT, Act>(P, X, K, M, plan, stream);
   }
@@ -1807,7 +1827,7 @@ int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStrea
   const int tpr = split_tiles_per_round(K);
   const int grid = (ntiles + tpr - 1) / tpr;
   if (P.count == 1 && proj_one_enabled()) {
-    const ProjOne one = {{P.w[0]}, {P.s[0]}, {P.y[0]}, {P.n[0]}, {P.tile_end[0]}, 1, P.ntiles};
+    const ProjOne one = shrink_table<1>(P);
     auto kern = w4a16_split_kernel<PACKED, NR, SVEC, CT, Act, ProjOne>;
     if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(kStreamWaves * 64), lds, stream, one, X, K, M);
