@@ -335,6 +335,33 @@ def test_multi_projection_equals_single(w4, orc, dev, M, packed):
         assert np.array_equal(down(ys[j]).reshape(M, N), refs[j]), (j, N)
 
 
+@pytest.mark.parametrize("Ns", [[3584, 3584], [4096, 512, 512], [6144, 2048, 16, 16], [37, 1000]])
+@pytest.mark.parametrize("M", [1, 8, 32])
+@pytest.mark.parametrize("packed", [False, True])
+def test_multi_projection_small_groups(w4, orc, dev, Ns, M, packed):
+    # the fused groups of the census (gate/up, q/k/v, qkv/z/b/a) travel in a
+    # table of 4: bit for bit equal to one call per projection
+    K = 1024
+    x = torch.from_numpy(orc.synth_act(0x4417 + M, M, K).view(np.int16)).to(dev).view(torch.bfloat16)
+    ws, ss, refs = [], [], []
+    for j, N in enumerate(Ns):
+        W, S = orc.synth_w4a16(0x7100 + 17 * j + N, N, K)
+        w, s, _ = up(dev, W, S, np.zeros((1, K), np.uint16))
+        if packed:
+            w = w4.repack(w, s, N, K)
+        ws.append(w)
+        ss.append(s)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        if packed:
+            w4.gemv_prepacked(w, x, N, K, M, y=y, variant="stream")
+        else:
+            w4.gemv(w, s, x, N, K, M, y=y, variant="stream")
+        refs.append(down(y).reshape(M, N))
+    ys = w4.gemv_multi(ws, ss, x, Ns, K, M, prepacked=packed)
+    for j, N in enumerate(Ns):
+        assert np.array_equal(down(ys[j]).reshape(M, N), refs[j]), (j, N)
+
+
 def test_multi_projection_rejects_bad_count(w4, dev):
     x = torch.zeros((1, 128), dtype=torch.bfloat16, device=dev)
     with pytest.raises(ValueError):
