@@ -1639,9 +1639,10 @@ int stream_occupancy() {
 }
 
 // Share of the tiles (per mille) left to dispatcher-balanced workgroups
-// after the persistent ones (CUDALM_W4A16_STREAM_TAIL; 0 = all static).
+// after the persistent ones (CUDALM_W4A16_STREAM_TAIL, measurement only;
+// 0 = all static, the default).
 int stream_tail_permille() {
-  static const int v = env_setting("CUDALM_W4A16_STREAM_TAIL", 150, 0, 900);
+  static const int v = env_setting("CUDALM_W4A16_STREAM_TAIL", 0, 0, 900);
   return v;
 }
 
@@ -1688,10 +1689,11 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   const int cap = cu_count() * per_cu;
   const int pwg = want < cap ? want : cap;
   int t_static = ntiles, grid = pwg;
-  // Tail workgroups: the last 15% of the tiles go to one-tile-per-wave
-  // workgroups beyond the persistent grid (LM head 27.5 -> 25.6 us at M = 1,
-  // 30.1 -> 29.7 us at M = 8 in graph replay; at M >= 16 their larger x
-  // staging makes it slower).
+  // Tail workgroups (off by default): the last share of the tiles goes to
+  // one-tile-per-wave workgroups beyond the persistent grid. With cached
+  // weight loads a 15% tail gained 1.4 us on the LM head at M = 1; with
+  // the non-temporal weight loads the all-static grid is faster (M = 1
+  // 23.12 -> 22.84 us, M = 8 25.28 -> 24.60 us against a 15% tail).
   const int tail_pm = M <= 8 ? stream_tail_permille() : 0;
   const int tail = static_cast<int>(static_cast<long long>(ntiles) * tail_pm / 1000);
   if (tail > 0 && ntiles - tail > pwg * WV) {
