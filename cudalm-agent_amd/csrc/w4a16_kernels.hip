@@ -610,6 +610,13 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
   }
 }
 
+// Read-only target of the stream kernel's last, unused piece load: 4 KB of
+// piece plus the lane spread, never written. Pointing that load here keeps
+// the loop's loads unconditional (a conditional load makes the compiler
+// wait for every load in flight at the merge) without re-reading a
+// non-temporally loaded piece from HBM; all waves share these lines in L2.
+__device__ __align__(256) uint8_t g_piece_sink[4 * 1024 + 64 * 16];
+
 // Piece streaming: the same arithmetic as the stream kernel (the 8-group
 // unit partial, then the unit sum), but weights are fetched and consumed in
 // pieces of HG groups (HG divides 8), so the compute that trails a wave's
@@ -733,9 +740,10 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
     const bool has_next = nt < ntiles;
     TileAddr anx = acur;
     if (has_next && nh == 0) anx = tile_addr<PACKED>(P, K, G, nt, lane);
-    // past the last piece, re-read the current one (cache hits) instead of
-    // branching around the loads
-    stream_load_piece<HG, PACKED, SVEC, FULL>(nxt, anx, G, (has_next ? nh : h) * HG);
+    // past the last piece, load from the sink instead of branching around
+    // the loads (the scales re-read the current tile's, cached)
+    if (!has_next) anx.w = g_piece_sink + lane * 16;
+    stream_load_piece<HG, PACKED, SVEC, FULL>(nxt, anx, G, (has_next ? nh : 0) * HG);
     const int g0 = h * HG;
     stream_piece<HG, NR, CT, Layout<Act, PACKED>, FULL, IOFF>(part, cur, xrow, corr, g0,
                                                              min(HG, G - g0), a);
