@@ -587,8 +587,10 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
       nt = t + stride;
     }
     const bool has_next = nt < ntiles;
-    // past the last unit, re-read the current one (cache hits) instead of
-    // branching around the loads
+    // past the last unit, re-read the current one instead of branching
+    // around the loads (with the non-temporal weight loads this re-read
+    // goes to HBM; this whole-unit kernel is kept as a measurement
+    // baseline, the piece kernel reads a sink there)
     stream_load_t<PACKED, SVEC>(nxt, P, K, G, has_next ? nt : t, has_next ? nu * kUnit : u * kUnit,
                                 lane);
     const int g0 = u * kUnit;
