@@ -392,3 +392,25 @@ def test_piece_split_equals_stream(w4, orc, dev, N, K, M):
         yp = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
         w4.gemv_prepacked(p, x, N, K, M, y=yp, variant=name)
         assert np.array_equal(down(yp).reshape(M, N), Y), ("prepacked", name)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_shapes_auto_equals_tile(w4, orc, dev, seed):
+    # seeded random shapes across the dispatch plans (piece split of every
+    # plan, unit split, stream, prefill GEMM, 16-row passes): the auto path,
+    # file layout and prepacked, against the tile kernel, bit for bit
+    rng = np.random.default_rng(0xD15 + seed)
+    for _ in range(6):
+        K = 128 * int(rng.integers(1, 33))
+        N = int(rng.integers(1, max(2, min(20000, (12 << 20) // K))))
+        M = int(rng.choice([1, 2, 3, 5, 8, 13, 16, 17, 24, 32, 33, 48]))
+        W, S = orc.synth_w4a16(int(rng.integers(1 << 30)), N, K)
+        X = orc.synth_act(int(rng.integers(1 << 30)), M, K)
+        w, s, x = up(dev, W, S, X)
+        ref = run(w4, w, s, x, N, K, M, "tile16")
+        got = run(w4, w, s, x, N, K, M)
+        assert np.array_equal(got, ref), ("auto", N, K, M)
+        p = w4.repack(w, s, N, K)
+        yp = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        w4.gemv_prepacked(p, x, N, K, M, y=yp)
+        assert np.array_equal(down(yp).reshape(M, N), ref), ("prepacked", N, K, M)
