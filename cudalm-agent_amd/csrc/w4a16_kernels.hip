@@ -131,10 +131,12 @@ __device__ __forceinline__ f32x4_t group_offset(const u32x4_t (&xa)[4]) {
 }
 
 // Activation / output element type of a kernel instance. Both encode a
-// weight nibble as the exact value 1.5 + q/16 in the activation's 16-bit
-// format, so the same offset cancellation and epilogue apply.
+// weight nibble as an exact value c + q/kUnit in the activation's 16-bit
+// format (the nibble in mantissa bits 3..6), cancel c with an MFMA against
+// -c, and scale the accumulated sum by kUnit in the epilogue.
 struct ActBf16 {
   static constexpr uint32_t kNegOffsetPair = 0xBFC0BFC0u;  // -1.5, -1.5
+  static constexpr float kUnit = 16.0f;  // weight element = 1.5 + q / kUnit
   template <bool ROT>
   __device__ static u32x4_t decode(uint32_t w) { return decode_nibbles<ROT>(w); }
   __device__ static f32x4_t mma(u32x4_t a, u32x4_t b, f32x4_t c) { return mfma16(a, b, c); }
@@ -142,25 +144,27 @@ struct ActBf16 {
   __device__ static float widen(uint32_t h) { return bf16_lo(h); }
 };
 
-// fp16: 1.0 = 0x3C00, 10 mantissa bits, so q/16 sits at bit 6 and the
-// biased nibble (q + 8 = nibble ^ 8) lands in bits 6..9: 0x3C00 | 0x0200
-// is 1.5, and nibble k moves to bit 6 of its half with one shift (one
-// rotation from the prepacked form, which is the file dword rotated left 3).
+// fp16: 1.0 = 0x3C00 with 10 mantissa bits, so the biased nibble (q + 8 =
+// nibble ^ 8) placed at bits 3..6, where bf16 puts it, is 1 + (q + 8)/128 =
+// 1.0625 + q/128 (0x3C00 | 0x0040 is 1.0625). The same shifts and masks as
+// bf16 decode it (7 VALU ops per prepacked dword); the offset is -1.0625 and
+// the epilogue multiplies by 128 instead of 16.
 struct ActF16 {
-  static constexpr uint32_t kNegOffsetPair = 0xBE00BE00u;  // -1.5, -1.5
+  static constexpr uint32_t kNegOffsetPair = 0xBC40BC40u;  // -1.0625, -1.0625
+  static constexpr float kUnit = 128.0f;
   template <bool ROT>
   __device__ static u32x4_t decode(uint32_t w) {
     u32x4_t a;
     if constexpr (ROT) {
-      a[0] = (rotr(w, 29) & 0x03C003C0u) ^ 0x3E003E00u;
-      a[1] = (rotr(w, 1) & 0x03C003C0u) ^ 0x3E003E00u;
-      a[2] = (rotr(w, 5) & 0x03C003C0u) ^ 0x3E003E00u;
-      a[3] = (rotr(w, 9) & 0x03C003C0u) ^ 0x3E003E00u;
+      a[0] = (w & 0x00780078u) ^ 0x3C403C40u;
+      a[1] = (rotr(w, 4) & 0x00780078u) ^ 0x3C403C40u;
+      a[2] = (rotr(w, 8) & 0x00780078u) ^ 0x3C403C40u;
+      a[3] = (rotr(w, 12) & 0x00780078u) ^ 0x3C403C40u;
     } else {
-      a[0] = ((w << 6) & 0x03C003C0u) ^ 0x3E003E00u;
-      a[1] = ((w << 2) & 0x03C003C0u) ^ 0x3E003E00u;
-      a[2] = ((w >> 2) & 0x03C003C0u) ^ 0x3E003E00u;
-      a[3] = ((w >> 6) & 0x03C003C0u) ^ 0x3E003E00u;
+      a[0] = ((w << 3) & 0x00780078u) ^ 0x3C403C40u;
+      a[1] = ((w >> 1) & 0x00780078u) ^ 0x3C403C40u;
+      a[2] = ((w >> 5) & 0x00780078u) ^ 0x3C403C40u;
+      a[3] = ((w >> 9) & 0x00780078u) ^ 0x3C403C40u;
     }
     return a;
   }
@@ -511,7 +515,7 @@ __device__ __forceinline__ void store_tile(const PT& P, int t, const f32x4_t (&t
     for (int r = 0; r < NR; ++r) {
       if (ct * 16 + 4 * a + r < M)
         col[static_cast<size_t>(ct * 16 + r) * Nj] =
-            static_cast<uint16_t>(Act::round(16.0f * total[ct][r]));
+            static_cast<uint16_t>(Act::round(Act::kUnit * total[ct][r]));
     }
 }
 
