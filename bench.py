@@ -237,7 +237,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the W4A16 projection path runs on a single "
-              "MI355X here (multi-GPU sharding along N is described in DESIGN.md, not run).",
+              "MI355X here (sharding along N across GPUs is a design, not built or run).",
               file=sys.stderr)
         sys.exit(2)
 
