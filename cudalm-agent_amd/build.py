@@ -16,14 +16,14 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB = os.path.join(PKG_DIR, "cudalm_w4a16", "libcudalm_w4a16.so")
-SOURCES = ["w4a16_kernels.hip", "bf16_gemv_kernels.hip", "w4a16_host.hip", "cudalm_v2_reader.cpp"]
+SOURCES = ["w4a16_kernels.hip", "w4a16_gemm.hip", "bf16_gemv_kernels.hip", "w4a16_host.hip",
+           "cudalm_v2_reader.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # packed fp32 VALU ops are kept out of all device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # explicit fp32 operation sequence: no mul+add contraction
@@ -41,20 +41,55 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def build(verbose: bool = False) -> str:
+def _stale(obj: str, src: str) -> bool:
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [src] + [os.path.join(d, f) for d in (CSRC, os.path.join(REPO, "include"))
+                    for f in os.listdir(d) if f.endswith(".h")]
+    deps += [os.path.join(REPO, "include", "cudalm", d, f)
+             for d in ("", "kernels") if os.path.isdir(os.path.join(REPO, "include", "cudalm", d))
+             for f in os.listdir(os.path.join(REPO, "include", "cudalm", d)) if f.endswith(".h")]
+    return any(os.path.getmtime(p) > t for p in deps)
+
+
+def build(verbose: bool = False, incremental: bool = False) -> str:
+    """Compile every source to an object in parallel (one hipcc per file),
+    then link the shared library. incremental: recompile only objects older
+    than their source or any header."""
     os.makedirs(os.path.dirname(LIB), exist_ok=True)
+    objdir = os.path.join(PKG_DIR, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    procs = []
+    objs = []
+    for src in SOURCES:
+        obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
+        objs.append(obj)
+        if incremental and not _stale(obj, os.path.join(CSRC, src)):
+            continue
+        cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(REPO, "include"), "-c",
+               os.path.join(CSRC, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                                            text=True)))
+    failed = []
+    for src, p in procs:
+        out, _ = p.communicate()
+        if p.returncode != 0:
+            sys.stderr.write(out)
+            failed.append(src)
+    if failed:
+        raise RuntimeError("hipcc failed on " + ", ".join(failed))
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(REPO, "include"),
-           *[os.path.join(CSRC, s) for s in SOURCES], "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed building libcudalm_w4a16.so")
+        raise RuntimeError("hipcc failed linking libcudalm_w4a16.so")
     os.replace(tmp, LIB)
     return LIB
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, incremental="--incremental" in sys.argv))

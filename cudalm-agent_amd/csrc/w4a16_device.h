@@ -1,0 +1,96 @@
+// W4A16 device helpers shared by the engine's kernel files (gfx950): the
+// weight-layout constants, the exact nibble -> bf16 decode, the activation
+// pair order and the MFMA offset chain that cancels the decode's 1.5 bias.
+#ifndef CUDALM_W4A16_DEVICE_H
+#define CUDALM_W4A16_DEVICE_H
+
+#include "hip_common.h"
+
+namespace cudalm_hip {
+
+constexpr int kGroup = 128;     // quantization group (k)
+constexpr int kTileRows = 16;   // weight rows per MFMA tile
+constexpr int kUnit = 8;        // groups per streamed unit
+constexpr uint32_t kNegOffsetPair = 0xBFC0BFC0u;  // bf16 -1.5 in both halves
+
+__host__ __device__ constexpr int packed_scale_pitch(int G) { return 16 * ((G + 7) / 8); }
+__host__ __device__ constexpr size_t packed_tile_bytes(int G) {
+  return static_cast<size_t>(G) * 1024 + 16 * static_cast<size_t>(packed_scale_pitch(G));
+}
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+// 8 nibbles (k = 0..7 of a block, nibble k at bits 4k) -> 4 bf16 pairs
+// (k, k+4), each element 1.5 + q/16. ROT: the dword is the prepacked form,
+// rotated left by 3 at load time, so pair 0 is already in place (one
+// v_bitop3) and pairs 1..3 need one v_alignbit each: 7 VALU ops instead of 8.
+__device__ __forceinline__ uint32_t rotr(uint32_t w, int s) {
+  return __builtin_amdgcn_alignbit(w, w, s);
+}
+
+template <bool ROT = false>
+__device__ __forceinline__ u32x4_t decode_nibbles(uint32_t w) {
+  u32x4_t a;
+  if constexpr (ROT) {
+    a[0] = (w & 0x00780078u) ^ 0x3FC03FC0u;
+    a[1] = (rotr(w, 4) & 0x00780078u) ^ 0x3FC03FC0u;
+    a[2] = (rotr(w, 8) & 0x00780078u) ^ 0x3FC03FC0u;
+    a[3] = (rotr(w, 12) & 0x00780078u) ^ 0x3FC03FC0u;
+  } else {
+    a[0] = ((w << 3) & 0x00780078u) ^ 0x3FC03FC0u;
+    a[1] = ((w >> 1) & 0x00780078u) ^ 0x3FC03FC0u;
+    a[2] = ((w >> 5) & 0x00780078u) ^ 0x3FC03FC0u;
+    a[3] = ((w >> 9) & 0x00780078u) ^ 0x3FC03FC0u;
+  }
+  return a;
+}
+
+// Prepacked form of a file dword of 8 nibbles (see decode_nibbles<true>).
+__host__ __device__ __forceinline__ uint32_t prepack_dword(uint32_t w) {
+  return (w << 3) | (w >> 29);
+}
+
+// Natural bf16 order [x0x1 x2x3 x4x5 x6x7] -> pair order [x0x4 x1x5 x2x6 x3x7].
+__device__ __forceinline__ u32x4_t pair_order(u32x4_t v) {
+  u32x4_t p;
+  // v_perm_b32 byte select over (hi:lo) = (v[2]:v[0]) and (v[3]:v[1]):
+  // p0 = lo16(v0) | lo16(v2) << 16, p1 = hi16(v0) | hi16(v2) << 16, ...
+  p[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+  p[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+  p[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+  p[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+  return p;
+}
+
+// -1.5 * (sum over the group of this lane-set's activation rows), as a 16x16
+// accumulator tile (all columns equal).
+__device__ __forceinline__ f32x4_t group_offset(const u32x4_t (&xa)[4]) {
+  const u32x4_t neg = {kNegOffsetPair, kNegOffsetPair, kNegOffsetPair, kNegOffsetPair};
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t c = mfma16(xa[0], neg, zero);
+  c = mfma16(xa[1], neg, c);
+  c = mfma16(xa[2], neg, c);
+  c = mfma16(xa[3], neg, c);
+  return c;
+}
+
+// Prefill-chunk GEMM (M >= 33) in w4a16_gemm.hip. cfg < 0 picks the tile
+// shape by problem size; other values force one (measurement only). Returns
+// a CUDALM_W4A16_* code, or 1 when cfg names no configuration of this
+// kernel (the caller then uses its own).
+template <bool PACKED>
+int launch_prefill_group(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
+                         int K, int M, int cfg, hipStream_t stream);
+
+// Registers per lane of the default prefill GEMM instance.
+int prefill_group_regs();
+
+}  // namespace cudalm_hip
+
+#endif

@@ -52,83 +52,12 @@
 
 #include "cudalm_w4a16.h"
 #include "hip_common.h"
+#include "w4a16_device.h"
 
 namespace {
 
 using namespace cudalm_hip;
 
-
-constexpr int kGroup = 128;     // quantization group (k)
-constexpr int kTileRows = 16;   // weight rows per MFMA tile
-constexpr int kUnit = 8;        // groups per streamed unit
-constexpr uint32_t kNegOffsetPair = 0xBFC0BFC0u;  // bf16 -1.5 in both halves
-
-__host__ __device__ constexpr int packed_scale_pitch(int G) { return 16 * ((G + 7) / 8); }
-__host__ __device__ constexpr size_t packed_tile_bytes(int G) {
-  return static_cast<size_t>(G) * 1024 + 16 * static_cast<size_t>(packed_scale_pitch(G));
-}
-
-// ---------------------------------------------------------------------------
-// device helpers
-// ---------------------------------------------------------------------------
-
-__device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
-  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
-}
-
-// 8 nibbles (k = 0..7 of a block, nibble k at bits 4k) -> 4 bf16 pairs
-// (k, k+4), each element 1.5 + q/16. ROT: the dword is the prepacked form,
-// rotated left by 3 at load time, so pair 0 is already in place (one
-// v_bitop3) and pairs 1..3 need one v_alignbit each: 7 VALU ops instead of 8.
-__device__ __forceinline__ uint32_t rotr(uint32_t w, int s) {
-  return __builtin_amdgcn_alignbit(w, w, s);
-}
-
-template <bool ROT = false>
-__device__ __forceinline__ u32x4_t decode_nibbles(uint32_t w) {
-  u32x4_t a;
-  if constexpr (ROT) {
-    a[0] = (w & 0x00780078u) ^ 0x3FC03FC0u;
-    a[1] = (rotr(w, 4) & 0x00780078u) ^ 0x3FC03FC0u;
-    a[2] = (rotr(w, 8) & 0x00780078u) ^ 0x3FC03FC0u;
-    a[3] = (rotr(w, 12) & 0x00780078u) ^ 0x3FC03FC0u;
-  } else {
-    a[0] = ((w << 3) & 0x00780078u) ^ 0x3FC03FC0u;
-    a[1] = ((w >> 1) & 0x00780078u) ^ 0x3FC03FC0u;
-    a[2] = ((w >> 5) & 0x00780078u) ^ 0x3FC03FC0u;
-    a[3] = ((w >> 9) & 0x00780078u) ^ 0x3FC03FC0u;
-  }
-  return a;
-}
-
-// Prepacked form of a file dword of 8 nibbles (see decode_nibbles<true>).
-__host__ __device__ __forceinline__ uint32_t prepack_dword(uint32_t w) {
-  return (w << 3) | (w >> 29);
-}
-
-// Natural bf16 order [x0x1 x2x3 x4x5 x6x7] -> pair order [x0x4 x1x5 x2x6 x3x7].
-__device__ __forceinline__ u32x4_t pair_order(u32x4_t v) {
-  u32x4_t p;
-  // v_perm_b32 byte select over (hi:lo) = (v[2]:v[0]) and (v[3]:v[1]):
-  // p0 = lo16(v0) | lo16(v2) << 16, p1 = hi16(v0) | hi16(v2) << 16, ...
-  p[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
-  p[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
-  p[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
-  p[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
-  return p;
-}
-
-// -1.5 * (sum over the group of this lane-set's activation rows), as a 16x16
-// accumulator tile (all columns equal).
-__device__ __forceinline__ f32x4_t group_offset(const u32x4_t (&xa)[4]) {
-  const u32x4_t neg = {kNegOffsetPair, kNegOffsetPair, kNegOffsetPair, kNegOffsetPair};
-  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f32x4_t c = mfma16(xa[0], neg, zero);
-  c = mfma16(xa[1], neg, c);
-  c = mfma16(xa[2], neg, c);
-  c = mfma16(xa[3], neg, c);
-  return c;
-}
 
 // Activation / output element type of a kernel instance. Both encode a
 // weight nibble as an exact value c + q/kUnit in the activation's 16-bit
@@ -2062,7 +1991,12 @@ template <bool PACKED>
 int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N, int K,
                    int M, hipStream_t stream) {
   int cfg = gemm_config();
-  if (cfg < 0) {
+  if (cfg < 0 || cfg >= 40) {
+    const int rc = launch_prefill_group<PACKED>(W, S, X, Y, N, K, M, cfg, stream);
+    if (rc != 1) return rc;
+    cfg = -1;
+  }
+  if (cfg == 1) {
     // unit GEMM: 128 x 32 workgroup tiles of 8 waves while they fill most
     // of the CUs, else 64 x 32 tiles of 4 waves, with two k-slices of 4 waves when
     // K spans several units (1024x3584 at M = 512: 16.7 -> 14.6 us). The
@@ -2377,7 +2311,7 @@ int cudalm_w4a16_kernel_regs(int variant) {
       return regs_of(w4a16_stream_piece_kernel<true, 1, false, 1, ActBf16, 4, true>);
     case CUDALM_W4A16_VARIANT_TILE16: return regs_of(w4a16_tile_kernel<1, 1, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_TILE32: return regs_of(w4a16_tile_kernel<1, 2, 4, 1, 8, true>);
-    case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_gemm_unit_kernel<1, 2, 8, true, false>);
+    case CUDALM_W4A16_VARIANT_PREFILL: return prefill_group_regs();
     case CUDALM_W4A16_VARIANT_BYTEWISE: return regs_of(w4a16_bytewise_kernel<ActBf16>);
     case CUDALM_W4A16_VARIANT_SPLIT: return regs_of(w4a16_split_kernel<true, 1, false, 1>);
     case CUDALM_W4A16_VARIANT_SWIGLU: return regs_of(w4a16_swiglu_kernel<true, 1, false, 1>);
