@@ -1,4 +1,7 @@
-// Prefill-chunk W4A16 GEMM (M >= 33) for MI355X (gfx950).
+// Pipelined prefill-chunk W4A16 GEMM for K = 1024 (MI355X, gfx950). A
+// measured alternative to the unit GEMM of w4a16_kernels.hip, selected only
+// by CUDALM_W4A16_GEMM_CFG = 50 / 51; it is not faster on the census shapes
+// at M = 512 (11-12 us against 10.7 us at 3584x1024), see the numbers below.
 //
 // Contract (reference: tests/cuda/test_int4_gemv_bf16.cpp:54-69 applied row
 // by row; the reference itself runs prefill one token at a time,
@@ -7,35 +10,26 @@
 //
 // Work decomposition. A workgroup of WN waves owns an output tile of
 // TN = WN * RN * 16 weight rows by TM = RM * 16 activation rows. Wave w owns
-// RN 16-row weight tiles and all RM 16-row activation tiles, so
-//   * each weight dword is decoded once per workgroup (by its owner) and
-//     feeds RM MFMAs (decode VALU per MFMA = 7 / RM);
-//   * each activation fragment read from LDS feeds RN MFMAs (LDS bytes per
-//     MFMA = 1 KB / RN).
-// K is walked one 128-k quantization group at a time. A group of the tile's
-// activations (TM rows x 256 B) is staged into one of two LDS buffers in
-// pair order while the previous group is computed; one barrier per group.
-// The wave that stages activation tile j also runs that tile's offset chain
-// (the four MFMAs of x against -1.5) from the same registers and parks it
-// in LDS beside the activations, so an offset chain is run once per
-// activation tile and group in the whole workgroup, not once per wave.
+// RN 16-row weight tiles and all RM activation tiles, so each weight dword
+// is decoded once per workgroup and feeds RM MFMAs, and each activation
+// fragment read from LDS feeds RN MFMAs. The 8 groups of the unit run as
+// straight-line code: the activations of the next groups arrive through a
+// 4-slot register ring (coalesced 64-byte row pieces, put back into MFMA
+// operand order by a cross-row lane transpose), each group is staged into
+// one of two LDS buffers in pair order with its offset chain, and one
+// barrier per group publishes it. Outputs leave through LDS as 16-byte rows.
 //
-// Weights and activations arrive through register rings: the weights of
-// group g + RW - 1 and the activations of group g + 1 + RX are requested
-// while group g is computed.
+// Per-output operation sequence (identical to every other W4A16 kernel of
+// this library, so the bits are the same): per group, tmp = offset chain,
+// then four MFMAs of x against the decoded weights seeded with it;
+// part = fma(s_g, tmp, part) from 0 in group order; y = bf16_rne(16 * (0 + part)).
 //
-// Per-output operation sequence (identical to the decode kernels): per
-// group, tmp = offset chain, then four MFMAs of x against the decoded
-// weights in k order seeded with it; part = fma(s_g, tmp, part) from 0 in
-// group order within an 8-group unit; total = total + part in unit order
-// from 0; y = bf16_rne(16 * total). The bits therefore equal those of every
-// other W4A16 kernel of this library.
-//
-// Workgroups are numbered so that each XCD (workgroups are dealt to the 8
-// XCDs round-robin) gets a contiguous run of weight tiles with all of their
-// activation blocks: each weight tile is read from HBM into one XCD's L2
-// only, and the activations (shared by all weight tiles) are what every
-// XCD reads.
+// Where the time goes (3584x1024x512, 224 workgroups of 4 waves, per-wave
+// s_memrealtime probes of the CUDALM_GEMM_PROBE build): about 2 us before
+// the first group (the L2 is cold at every dispatch: TCC misses fetch x once
+// per XCD, ~10.9 MB per launch), 8 groups of ~0.65-0.75 us each (32 MFMAs,
+// ~130 VALU, the staging and one barrier; the MFMAs alone are ~0.3 us at the
+// measured 8.75 ns per 16x16x32 MFMA of one wave), and ~0.9 us of output.
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -55,14 +49,10 @@ constexpr int kXcds = 8;
 __device__ unsigned long long g_probe[4096 * 8 * 8];
 #define GEMM_PROBE(k)                                                           \
   if (lane == 0 && blockIdx.x < 4096)                                           \
-  g_probe[(blockIdx.x * 8 + wv + 4 * rep) * 8 + (k)] = __builtin_amdgcn_s_memrealtime()
-constexpr int kProbeReps = 2;  // tiles per workgroup, to compare a cold and a warm pass
+  g_probe[(blockIdx.x * 8 + wv) * 8 + (k)] = __builtin_amdgcn_s_memrealtime()
 #else
-constexpr int kProbeReps = 1;
 #define GEMM_PROBE(k)
 #endif
-
-constexpr int kHalf = kUnit / 2;  // groups per staged half unit
 
 // 4 x 4 transpose across the wave's 16-lane rows: afterwards r[d] of row a
 // holds what r[a] of row d held. Two v_permlane32_swap and two
@@ -83,37 +73,51 @@ __device__ __forceinline__ void transpose4(u32x4_t (&r)[4]) {
   }
 }
 
-// ONE: K fits one 8-group unit (no cross-unit sum is kept).
-template <int WN, int RN, int RM, bool PACKED, bool SVEC, bool ONE>
-__global__ __launch_bounds__(WN * 64) void w4a16_gemm_lds_kernel(
+// Pipelined variant for K = 1024 (one 8-group unit, the census's common
+// case): straight-line code over the 8 groups. Activations of the next
+// groups arrive through a 4-slot register ring while the current group is
+// computed; each group is staged into one of two LDS buffers (pair order,
+// offset chain by the staging wave) and published with one barrier. All
+// weights and scales of the unit are requested up front.
+template <int WN, int RN, int RM, bool PACKED, bool SVEC>
+__global__ __launch_bounds__(WN * 64) void w4a16_gemm_pipe_kernel(
     const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
-    const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, int N, int K, int M, int gmb) {
+    const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, int N, int M, int gmb) {
+  constexpr int K = kUnit * kGroup, G = kUnit;
   constexpr int TM = RM * 16;
   constexpr int TN = WN * RN * 16;
-  constexpr int SPW = (RM + WN - 1) / WN;  // activation tiles staged per wave (j = wv + s WN < RM)
-  // LDS: activation chunks [RM][kUnit][4][64] x 16 B (chunk (j, g, d) holds
-  // lane l's MFMA operand of activation tile j, group g, step d at 16 l, in
-  // pair order), then the offset table [kUnit][TM] floats
+  constexpr int SPW = (RM + WN - 1) / WN;
+  constexpr int RX = 4;  // activation ring (groups)
+  // LDS: two group buffers [2][RM][4][64] x 16 B, offsets [2][TM] floats;
+  // the output tile [TM][TN + 8] bf16 reuses the group buffers at the end
   extern __shared__ u32x4_t lds[];
   u32x4_t* xs = lds;
-  float* offs = reinterpret_cast<float*>(lds + RM * kUnit * 4 * 64);
+  float* offs = reinterpret_cast<float*>(lds + 2 * RM * 4 * 64);
 
-  const int G = K >> 7;
-  const int U = ONE ? 1 : (G + kUnit - 1) / kUnit;
   const int ntiles = (N + kTileRows - 1) / kTileRows;
   const int lane = threadIdx.x & 63;
   const int i = lane & 15, a = lane >> 4;
   const int wv = wave_id();
-  for (int rep = 0; rep < kProbeReps; ++rep) {
   GEMM_PROBE(0);
-
-  // XCD-aware numbering: hardware slot L runs on XCD L % 8; XCD x gets the
-  // contiguous run [x * T / 8, (x + 1) * T / 8) of the (weight block major,
-  // activation block minor) order.
-  const int T = static_cast<int>(gridDim.x) * kProbeReps;
-  const int L = static_cast<int>(blockIdx.x) * kProbeReps + rep;
-  const int lin = (T % kXcds == 0) ? (L % kXcds) * (T / kXcds) + L / kXcds : L;
-  const int nb = lin / gmb, mb = lin - nb * gmb;
+  // XCD-aware numbering (hardware slot L runs on XCD L % 8). When the
+  // tile grid splits evenly, XCD x takes a block of gnb/4 weight blocks by
+  // gmb/2 activation blocks, which is about the fewest bytes one XCD's L2
+  // must pull in; otherwise a contiguous run of the weight-major order.
+  const int T = static_cast<int>(gridDim.x);
+  const int L = static_cast<int>(blockIdx.x);
+  const int gnb = T / gmb;
+  int nb, mb;
+  if (T % kXcds == 0 && gmb % 2 == 0 && gnb % 4 == 0) {
+    const int xcd = L % kXcds, slot = L / kXcds;
+    const int mbs = gmb / 2, nbs = gnb / 4;
+    const int nn = slot / mbs;
+    nb = (xcd >> 1) * nbs + nn;
+    mb = (xcd & 1) * mbs + (slot - nn * mbs);
+  } else {
+    const int lin = (T % kXcds == 0) ? (L % kXcds) * (T / kXcds) + L / kXcds : L;
+    nb = lin / gmb;
+    mb = lin - nb * gmb;
+  }
   const int m0 = mb * TM;
   const int mrows = min(TM, M - m0);
 
@@ -133,160 +137,143 @@ __global__ __launch_bounds__(WN * 64) void w4a16_gemm_lds_kernel(
       sl[rn] = reinterpret_cast<const uint8_t*>(S + static_cast<size_t>(row) * G);
     }
   }
-  constexpr int kStep = PACKED ? 1024 : 64;  // bytes between groups of one lane
+  constexpr int kStep = PACKED ? 1024 : 64;
   const uint16_t* xrow[SPW];
 #pragma unroll
   for (int s = 0; s < SPW; ++s)
     xrow[s] = X + static_cast<size_t>(m0 + min(16 * min(wv + s * WN, RM - 1) + i, mrows - 1)) * K +
               8 * a;
 
-  // this wave's activations of groups g0 .. g0+3 (indices clamped). Load q
-  // of lane (i, c) reads row i, 16-byte block 4q + c of the group, so the
-  // four lanes of a row read 64 contiguous bytes; transpose4() then gives
-  // lane (i, a) its MFMA operand blocks 4a .. 4a+3.
-  auto load_half = [&](u32x4_t (&dst)[SPW][kHalf][4], int g0) {
+  // load d of lane (i, c) reads row i, 16-byte block 4d + c of the group (the
+  // four lanes of a row read 64 contiguous bytes); transpose4() then gives
+  // lane (i, a) its own MFMA operand blocks 4a .. 4a+3
+  u32x4_t xr[RX][SPW][4];
+  auto load_x = [&](u32x4_t (&dst)[SPW][4], int g) {
 #pragma unroll
     for (int s = 0; s < SPW; ++s)
 #pragma unroll
-      for (int gg = 0; gg < kHalf; ++gg)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          dst[s][gg][q] = *reinterpret_cast<const u32x4_t*>(xrow[s] + min(g0 + gg, G - 1) * kGroup +
-                                                            32 * q);
+      for (int d = 0; d < 4; ++d)
+        dst[s][d] = *reinterpret_cast<const u32x4_t*>(xrow[s] + g * kGroup + 32 * d);
   };
-  // pair order, park in LDS, and the offset chains from the same registers
-  auto stage_half = [&](const u32x4_t (&src)[SPW][kHalf][4], int h) {
+  // the next group in pair order with its offset chains, in registers ...
+  struct Staged {
+    u32x4_t xa[SPW][4];
+    f32x4_t o[SPW];
+  };
+  auto prepare = [&](Staged& st, const u32x4_t (&src)[SPW][4]) {
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      if (wv + s * WN >= RM) continue;  // wave-uniform
+      u32x4_t r[4] = {src[s][0], src[s][1], src[s][2], src[s][3]};
+      transpose4(r);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) st.xa[s][d] = pair_order(r[d]);
+      st.o[s] = group_offset(st.xa[s]);
+    }
+  };
+  // ... and parked in LDS buffer b
+  auto publish = [&](const Staged& st, int b) {
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
       const int j = wv + s * WN;
       if (j >= RM) continue;  // wave-uniform
+      u32x4_t* blk = xs + ((b * RM + j) * 4) * 64 + lane;
 #pragma unroll
-      for (int q = 0; q < kHalf; ++q) {
-        const int gg = h * kHalf + q;
-        u32x4_t xa[4] = {src[s][q][0], src[s][q][1], src[s][q][2], src[s][q][3]};
-        transpose4(xa);
-#pragma unroll
-        for (int d = 0; d < 4; ++d) xa[d] = pair_order(xa[d]);
-        u32x4_t* blk = xs + ((j * kUnit + gg) * 4) * 64 + lane;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) blk[d * 64] = xa[d];
-        const f32x4_t o = group_offset(xa);
-        if (i == 0) *reinterpret_cast<f32x4_t*>(offs + gg * TM + 16 * j + 4 * a) = o;
-      }
+      for (int d = 0; d < 4; ++d) blk[d * 64] = st.xa[s][d];
+      if (i == 0) *reinterpret_cast<f32x4_t*>(offs + b * TM + 16 * j + 4 * a) = st.o[s];
     }
   };
 
+  // prologue: activations of groups 0 .. 3, then every weight and scale
+#pragma unroll
+  for (int q = 0; q < RX; ++q) load_x(xr[q], q);
+  u32x4_t w[RN][G];
+  u32x4_t sc[RN];
+#pragma unroll
+  for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+    for (int rn = 0; rn < RN; ++rn)
+      w[rn][gg] = *reinterpret_cast<const u32x4_t*>(wl[rn] + static_cast<size_t>(gg) * kStep);
+#pragma unroll
+  for (int rn = 0; rn < RN; ++rn) {
+    if constexpr (PACKED || SVEC) {
+      sc[rn] = *reinterpret_cast<const u32x4_t*>(sl[rn]);
+    } else {
+      const uint16_t* srow = reinterpret_cast<const uint16_t*>(sl[rn]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        sc[rn][q] = static_cast<uint32_t>(srow[2 * q]) | (static_cast<uint32_t>(srow[2 * q + 1]) << 16);
+    }
+  }
+  GEMM_PROBE(1);
+  Staged st;
+  prepare(st, xr[0]);
+  publish(st, 0);
+  load_x(xr[0], RX);
+  __syncthreads();
+  GEMM_PROBE(2);
+
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f32x4_t acc[RN][RM], part[RN][RM];
+  f32x4_t part[RN][RM];
 #pragma unroll
   for (int rn = 0; rn < RN; ++rn)
 #pragma unroll
-    for (int ct = 0; ct < RM; ++ct) acc[rn][ct] = zero;
-
-  for (int u = 0; u < U; ++u) {
-    const int g0 = u * kUnit;
-    const int gn = min(kUnit, G - g0);
-    u32x4_t xr[SPW][kHalf][4];
-    load_half(xr, g0);
-    // the unit's weights and scales (group indices clamped to G - 1)
-    u32x4_t w[RN][kUnit];
-    u32x4_t sc[RN];
+    for (int ct = 0; ct < RM; ++ct) part[rn][ct] = zero;
 #pragma unroll
-    for (int rn = 0; rn < RN; ++rn) {
-#pragma unroll
-      for (int gg = 0; gg < kUnit; ++gg)
-        w[rn][gg] = *reinterpret_cast<const u32x4_t*>(
-            wl[rn] + static_cast<size_t>(min(g0 + gg, G - 1)) * kStep);
-      if constexpr (PACKED || SVEC) {
-        sc[rn] = *reinterpret_cast<const u32x4_t*>(sl[rn] + 2 * g0);
-      } else {
-        const uint16_t* srow = reinterpret_cast<const uint16_t*>(sl[rn]);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          sc[rn][q] = static_cast<uint32_t>(srow[min(g0 + 2 * q, G - 1)]) |
-                      (static_cast<uint32_t>(srow[min(g0 + 2 * q + 1, G - 1)]) << 16);
-      }
+  for (int gg = 0; gg < G; ++gg) {
+    const int b = gg & 1;
+    // the next group's transform and offset chains interleave with this group's MFMAs
+    if (gg + 1 < G) {
+      prepare(st, xr[(gg + 1) % RX]);
+      if (gg + 1 + RX < G) load_x(xr[(gg + 1) % RX], gg + 1 + RX);
     }
-    GEMM_PROBE(1);
-    if (u > 0) __syncthreads();  // the previous unit's readers are done
-    stage_half(xr, 0);
-    if (gn > kHalf) load_half(xr, g0 + kHalf);
-    GEMM_PROBE(2);
-    __syncthreads();
-    GEMM_PROBE(3);
-
+    f32x4_t t[RN][RM];
 #pragma unroll
-    for (int rn = 0; rn < RN; ++rn)
+    for (int ct = 0; ct < RM; ++ct) {
+      const f32x4_t o = *reinterpret_cast<const f32x4_t*>(offs + b * TM + 16 * ct + 4 * a);
 #pragma unroll
-      for (int ct = 0; ct < RM; ++ct) part[rn][ct] = zero;
-    auto group = [&](int gg) {
-      f32x4_t t[RN][RM];
+      for (int rn = 0; rn < RN; ++rn) t[rn][ct] = o;
+    }
 #pragma unroll
-      for (int ct = 0; ct < RM; ++ct) {
-        const f32x4_t o = *reinterpret_cast<const f32x4_t*>(offs + gg * TM + 16 * ct + 4 * a);
+    for (int d = 0; d < 4; ++d) {
+      u32x4_t xa[RM];
 #pragma unroll
-        for (int rn = 0; rn < RN; ++rn) t[rn][ct] = o;
-      }
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        u32x4_t xa[RM];
-#pragma unroll
-        for (int ct = 0; ct < RM; ++ct) xa[ct] = xs[((ct * kUnit + gg) * 4 + d) * 64 + lane];
-#pragma unroll
-        for (int rn = 0; rn < RN; ++rn) {
-          const u32x4_t B = decode_nibbles<PACKED>(w[rn][gg][d]);
-#pragma unroll
-          for (int ct = 0; ct < RM; ++ct) t[rn][ct] = mfma16(xa[ct], B, t[rn][ct]);
-        }
-      }
+      for (int ct = 0; ct < RM; ++ct) xa[ct] = xs[((b * RM + ct) * 4 + d) * 64 + lane];
 #pragma unroll
       for (int rn = 0; rn < RN; ++rn) {
-        const float s = half_bits_to_f32((sc[rn][gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
+        const u32x4_t B = decode_nibbles<PACKED>(w[rn][gg][d]);
 #pragma unroll
-        for (int ct = 0; ct < RM; ++ct)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            part[rn][ct][r] = __builtin_fmaf(s, t[rn][ct][r], part[rn][ct][r]);
-      }
-    };
-    // first half while the second half's activations arrive
-    if (gn >= kHalf) {
-#pragma unroll
-      for (int gg = 0; gg < kHalf; ++gg) group(gg);
-    } else {
-#pragma unroll
-      for (int gg = 0; gg < kHalf; ++gg)
-        if (gg < gn) group(gg);
-    }
-    GEMM_PROBE(4);
-    if (gn > kHalf) {
-      stage_half(xr, 1);
-      __syncthreads();
-      if (gn == kUnit) {
-#pragma unroll
-        for (int gg = kHalf; gg < kUnit; ++gg) group(gg);
-      } else {
-#pragma unroll
-        for (int gg = kHalf; gg < kUnit; ++gg)
-          if (gg < gn) group(gg);
+        for (int ct = 0; ct < RM; ++ct) t[rn][ct] = mfma16(xa[ct], B, t[rn][ct]);
       }
     }
 #pragma unroll
-    for (int rn = 0; rn < RN; ++rn)
+    for (int rn = 0; rn < RN; ++rn) {
+      const float s = half_bits_to_f32((sc[rn][gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
 #pragma unroll
-      for (int ct = 0; ct < RM; ++ct) acc[rn][ct] = acc[rn][ct] + part[rn][ct];
+      for (int ct = 0; ct < RM; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          part[rn][ct][r] = __builtin_fmaf(s, t[rn][ct][r], part[rn][ct][r]);
+    }
+    if (gg == 3) GEMM_PROBE(3);
+    if (gg + 1 < G) publish(st, b ^ 1);
+    if (gg == 3) GEMM_PROBE(4);
+    __syncthreads();
+    if (gg == 3) GEMM_PROBE(7);
   }
   GEMM_PROBE(5);
 
-  // outputs. Lane (i, a) holds rows 4a .. 4a+3 of each activation tile,
-  // column i of each weight tile. When rows are 16-byte aligned the tile
-  // goes through LDS ([TM][TN + 8] bf16) and leaves as 16-byte row pieces.
+  // outputs: total = 0 + part (the canonical unit sum), then as in the unit kernel
+  f32x4_t acc[RN][RM];
+#pragma unroll
+  for (int rn = 0; rn < RN; ++rn)
+#pragma unroll
+    for (int ct = 0; ct < RM; ++ct) acc[rn][ct] = zero + part[rn][ct];
   const int n0 = nb * TN;
   const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
   if (vec) {
-    constexpr int OP = TN + 8;  // row pitch in bf16 (16 B pad)
+    constexpr int OP = TN + 8;
     uint16_t* ot = reinterpret_cast<uint16_t*>(lds);
-    __syncthreads();  // every wave is done reading activations
 #pragma unroll
     for (int rn = 0; rn < RN; ++rn) {
       const int c = (wv * RN + rn) * 16 + i;
@@ -298,7 +285,7 @@ __global__ __launch_bounds__(WN * 64) void w4a16_gemm_lds_kernel(
               static_cast<uint16_t>(f32_to_bf16_rne(16.0f * acc[rn][ct][r]));
     }
     __syncthreads();
-    constexpr int PR = TN / 8;  // 16-byte pieces per row
+    constexpr int PR = TN / 8;
     const int ncols = min(TN, N - n0);
     for (int e = threadIdx.x; e < TM * PR; e += WN * 64) {
       const int row = e / PR, pc = e - row * PR;
@@ -322,28 +309,25 @@ __global__ __launch_bounds__(WN * 64) void w4a16_gemm_lds_kernel(
     }
   }
   GEMM_PROBE(6);
-  __syncthreads();
-  }
 }
 
 template <int WN, int RN, int RM, bool PACKED>
-int launch_lds(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N, int K,
-               int M, hipStream_t stream) {
+int launch_pipe(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N, int K,
+                int M, hipStream_t stream) {
+  if (K != kUnit * kGroup) return 1;
   constexpr int TN = WN * RN * kTileRows, TM = RM * 16;
   const long long gnb = (N + TN - 1) / TN, gmb = (M + TM - 1) / TM;
   const long long T = gnb * gmb;
   if (T > 0x7FFFFFFFLL) return CUDALM_W4A16_ERANGE;
-  const int G = K / kGroup;
-  const bool svec = !PACKED && G % 8 == 0 && aligned(S, 16);
-  const size_t lds = static_cast<size_t>(RM) * kUnit * 4 * 64 * 16 + kUnit * TM * sizeof(float);
-  const bool one = G <= kUnit;
-  auto kern = svec ? (one ? w4a16_gemm_lds_kernel<WN, RN, RM, PACKED, true, true>
-                          : w4a16_gemm_lds_kernel<WN, RN, RM, PACKED, true, false>)
-                   : (one ? w4a16_gemm_lds_kernel<WN, RN, RM, PACKED, false, true>
-                          : w4a16_gemm_lds_kernel<WN, RN, RM, PACKED, false, false>);
+  const bool svec = !PACKED && aligned(S, 16);
+  const size_t xb = static_cast<size_t>(2) * RM * 4 * 64 * 16 + 2 * TM * sizeof(float);
+  const size_t ob = static_cast<size_t>(TM) * (TN + 8) * 2;
+  const size_t lds = xb > ob ? xb : ob;
+  auto kern = svec ? w4a16_gemm_pipe_kernel<WN, RN, RM, PACKED, true>
+                   : w4a16_gemm_pipe_kernel<WN, RN, RM, PACKED, false>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(T / kProbeReps)), dim3(WN * 64), lds, stream, W, S, X, Y,
-                     N, K, M, static_cast<int>(gmb));
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(T)), dim3(WN * 64), lds, stream, W, S, X, Y, N,
+                     M, static_cast<int>(gmb));
   return launch_status();
 }
 
@@ -354,17 +338,13 @@ int launch_prefill_group(const uint8_t* W, const uint16_t* S, const uint16_t* X,
                          int K, int M, int cfg, hipStream_t stream) {
   if (cfg < 0) return 1;  // by shape: the unit GEMM of the main kernel file
   switch (cfg) {
-    case 40: return launch_lds<4, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);  // 128 x 64
-    case 41: return launch_lds<4, 1, 4, PACKED>(W, S, X, Y, N, K, M, stream);  // 64 x 64
-    case 42: return launch_lds<2, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);  // 64 x 64, 2 waves
-    case 43: return launch_lds<2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);  // 64 x 32
-    case 44: return launch_lds<4, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);  // 128 x 32
-    case 45: return launch_lds<2, 1, 2, PACKED>(W, S, X, Y, N, K, M, stream);  // 32 x 32
+    case 50: return launch_pipe<4, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);  // 128 x 64
+    case 51: return launch_pipe<4, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);  // 128 x 32
     default: return 1;
   }
 }
 
-int prefill_group_regs() { return regs_of(w4a16_gemm_lds_kernel<4, 2, 4, true, false, true>); }
+int prefill_group_regs() { return regs_of(w4a16_gemm_pipe_kernel<4, 2, 4, true, false>); }
 
 #ifdef CUDALM_GEMM_PROBE
 extern "C" int cudalm_gemm_probe_read(void* host, size_t bytes) {

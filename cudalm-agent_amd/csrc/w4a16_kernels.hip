@@ -1994,7 +1994,7 @@ int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint1
   if (cfg < 0 || cfg >= 40) {
     const int rc = launch_prefill_group<PACKED>(W, S, X, Y, N, K, M, cfg, stream);
     if (rc != 1) return rc;
-    cfg = -1;
+    cfg = 1;
   }
   if (cfg == 1) {
     // unit GEMM: 128 x 32 workgroup tiles of 8 waves while they fill most
