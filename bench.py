@@ -81,6 +81,26 @@ def measured_traffic():
     return None
 
 
+PROFILE_CENSUS = "profiles/w4a16_census_kernel_trace.md"
+
+
+def census_kernel_sum_us(key: str):
+    """(summed kernel durations, graph wall) in us of one census traversal
+    `key` (M1, M1_fused, ...), both from the same run of the committed
+    rocprofv3 kernel-trace summary, or None."""
+    vals = {}
+    try:
+        for line in open(os.path.join(REPO, PROFILE_CENSUS)):
+            for tag in ("sum_kernel_us", "traced_wall_us"):
+                if line.startswith(f"{tag}[{key}] = "):
+                    vals[tag] = float(line.split("=")[1])
+    except OSError:
+        return None
+    if len(vals) != 2:
+        return None
+    return vals["sum_kernel_us"], vals["traced_wall_us"]
+
+
 def census_groups(fused: bool):
     """Launch groups of one decode step in call order. Fused groups are the
     projections that read the same activations (in_proj_qkv/z/b/a, gate/up,
@@ -225,6 +245,11 @@ def main():
                     help="headline workload only (for counter collection)")
     ap.add_argument("--bf16-lm-head-only", action="store_true",
                     help="only the tied bf16 LM head lines (for counter collection)")
+    ap.add_argument("--only", default="", choices=["", "config0", "lm_head_m8", "lm_head_m32"],
+                    help="kernel-trace / counter run: the headline, then only this side line")
+    ap.add_argument("--census-mode", default="", metavar="KEY",
+                    help="kernel-trace run: only the census traversal KEY (M1, M1_fused, M8, ...),"
+                         " graph-replayed as in the full run, then exit")
     ap.add_argument("--prefill-only", action="store_true",
                     help="headline plus the M = 512 prefill lines (for counter collection)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -234,6 +259,10 @@ def main():
         args.no_census = args.no_prefill = args.no_cpu = args.no_next = True
     if args.prefill_only:
         args.no_census = args.no_cpu = args.no_next = True
+    if args.census_mode or args.only:
+        args.no_prefill = args.no_cpu = args.no_next = True
+    if args.only:
+        args.no_census = True
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the W4A16 projection path runs on a single "
@@ -310,9 +339,11 @@ def main():
 
     extra = {}
     # ---------------- small-M batched decode on the LM head (M = 8, 32) ----------------
-    if not args.lm_head_only:
+    if not args.lm_head_only and not args.census_mode and args.only in ("", "lm_head_m8", "lm_head_m32"):
         small = {}
         for Mb in (8, 32):
+            if args.only and args.only != f"lm_head_m{Mb}":
+                continue
             xb = synth_act(torch, Mb, K, 0x11B0 + Mb, dev)
             yb = torch.empty((Mb, N), dtype=torch.bfloat16, device=dev)
             xbp, ybp = xb.data_ptr(), yb.data_ptr()
@@ -325,14 +356,14 @@ def main():
                                "algorithmic_bytes": nb}
         extra["lm_head_small_m"] = small
     file_per = float("nan")
-    if not args.lm_head_only:
+    if not args.lm_head_only and not args.census_mode and not args.only:
         file_per = stream_time(torch, [mk_file(w, s) for w, s in zip(ws, ss)],
                                min(args.steps, 100), args.warmup, stream)
     file_gbs = nbytes / file_per / 1e9 if file_per == file_per else None
 
     # M = 1, N = 3584, K = 1024 (rotate 64 copies = 120 MB; a
     cfg0_s = None
-    if not args.lm_head_only:
+    if not args.lm_head_only and not args.census_mode and args.only in ("", "config0"):
         # single 1.9 MB matrix would be served from cache)
         N0, K0 = 3584, 1024
         c0 = []
@@ -357,6 +388,8 @@ def main():
             cf[(li, name)] = (w, s)
         census = {}
         for Mc in (1, 8, 32):
+            if args.census_mode and not args.census_mode.startswith(f"M{Mc}"):
+                continue
             xs = {Kc: synth_act(torch, Mc, Kc, 0xAC70 + Kc + Mc, dev) for Kc in (1024, 2048, 3584)}
             ys = {(li, name): torch.empty((Mc, Nc), dtype=torch.bfloat16, device=dev)
                   for li, name, Nc, Kc in calls}
@@ -364,6 +397,9 @@ def main():
             yh = torch.empty((Mc, N), dtype=torch.bfloat16, device=dev)
             tot_bytes = sum(algo_bytes(Nc, Kc, Mc) for _, _, Nc, Kc in calls) + algo_bytes(N, K, Mc)
             for fused in (False, True):
+                key = f"M{Mc}" + ("_fused" if fused else "")
+                if args.census_mode and args.census_mode != key:
+                    continue
                 launches = []  # (list of (packed_ptr, y_ptr, N), K)
                 for group in census_groups(fused):
                     Kc = group[0][3]
@@ -384,14 +420,35 @@ def main():
                                                              Kc, Mc, 1, sraw)
 
                 t = graph_time(torch, traversal, 10, stream)
-                census[f"M{Mc}" + ("_fused" if fused else "")] = {
+                if args.census_mode:
+                    # 1 eager + 3 warm + 10 timed traversals were dispatched
+                    print(json.dumps({"census_mode": key, "launches": len(arrays),
+                                      "traversals_dispatched": 14,
+                                      "us_per_decode_step": round(t * 1e6, 2)}), flush=True)
+                    return
+                census[key] = {
                     "us_per_decode_step": round(t * 1e6, 2),
                     "launches": len(arrays),
                     "bytes": tot_bytes,
                     "GBps": round(tot_bytes / t / 1e9, 1),
                     "frac_hbm_peak": round(tot_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
                 }
-            if Mc == 1:
+                prof = census_kernel_sum_us(key)
+                if prof:
+                    # census roofline: summed kernel durations against the graph
+                    # wall of the same traversal, both from the committed
+                    # rocprofv3 kernel trace (the tracer lengthens every dispatch,
+                    # so the ratio is taken within the traced run)
+                    ksum, twall = prof
+                    census[key].update({
+                        "sum_kernel_us_traced": ksum,
+                        "graph_wall_us_traced": twall,
+                        "kernel_fraction_of_wall_traced": round(ksum / twall, 3),
+                        "GBps_over_sum_kernel": round(tot_bytes / (ksum * 1e-6) / 1e9, 1),
+                        "frac_hbm_peak_over_sum_kernel": round(tot_bytes / (ksum * 1e-6) / 1e9
+                                                               / HBM_PEAK_GBS, 4),
+                        "source": PROFILE_CENSUS})
+            if Mc == 1 and not args.census_mode:
                 # the drop-in case: the reference's 187 call sites unchanged,
                 # file-layout weights (no repack), one launch per projection
                 fl = [(cf[(li, nm)][0].data_ptr(), cf[(li, nm)][1].data_ptr(),
@@ -485,14 +542,33 @@ def main():
         Wn = ws[0].cpu().numpy()
         Sn = ss[0].view(torch.int16).cpu().numpy().view(np.uint16)
         Xn = x.view(torch.int16).cpu().numpy().view(np.uint16)
-        threads = min(oracle.hardware_threads(), 16)
+        # the GPU boxes allot 16 host threads per GPU, whatever the host reports
+        avail = oracle.hardware_threads()
+        threads = min(avail, 16)
         one = oracle.time_gemv_bf16(Wn, Sn, Xn, N, K, 1, threads, 1)
         iters = max(1, int(args.cpu_seconds / max(one, 1e-3)))
         t_cpu = oracle.time_gemv_bf16(Wn, Sn, Xn, N, K, 1, threads, iters)
         cpu = {"value": round(nbytes / t_cpu / 1e9, 2), "unit": "GB/s", "cores": threads,
+               "cores_available": avail,
                "kind": "port",
                "sample": f"full LM-head GEMV (N={N}, K={K}, M=1), {iters} calls after 1 warm-up, "
-                         f"rows split over {threads} threads; {t_cpu * 1e3:.1f} ms per call"}
+                         f"rows split over {threads} threads (the box's 16-thread share per GPU; "
+                         f"the host reports {avail}); {t_cpu * 1e3:.1f} ms per call"}
+        # parity of the timed headline kernel: y from packs[0] against the
+        # fp64 bound and against the reference's own CPU loop (ref_gemv_bf16)
+        lib.cudalm_w4a16_gemv_bf16_prepacked(packs[0].data_ptr(), xp, yp, N, K, M, sraw)
+        torch.cuda.synchronize()
+        Yg = y.view(torch.int16).cpu().numpy().view(np.uint16).reshape(M, N)
+        r64, a64 = oracle.gemv_f64(Wn, Sn, Xn, N, K, M)
+        ok, st = oracle.check_tolerance_f64(Yg, r64, a64, M, N)
+        Yr = oracle.gemv_bf16(Wn, Sn, Xn, N, K, M, threads)
+        _, st_ref = oracle.check_tolerance_f64(Yr, r64, a64, M, N)
+        diff = np.abs(oracle.bf16_to_f32(Yg).astype(np.float64) - oracle.bf16_to_f32(Yr).astype(np.float64))
+        cpu["parity"] = {"within_tolerance": bool(ok), "max_ulp_vs_fp64": round(st["max_ulp"], 3),
+                         "n_over_2ulp": st["n_over_2ulp"], "n": st["n"],
+                         "ref_cpu_loop_max_ulp_vs_fp64": round(st_ref["max_ulp"], 3),
+                         "n_differ_from_ref_cpu_loop": int((Yg != Yr).sum()),
+                         "max_abs_diff_vs_ref_cpu_loop": float(diff.max())}
         # single-core form of the reference's loop, on a bounded row sample
         rows = 16384
         t1 = oracle.time_gemv_bf16(Wn[:rows].copy(), Sn[:rows].copy(), Xn, rows, K, 1, 1, 3)

@@ -42,6 +42,7 @@ _SIGS = {
     "orc_gemv_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64], None),
     "orc_gemv_bf16_mt": ([_P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
     "orc_gemv_f64": ([_P, _P, _P, _P, _P, _I64, _I64, _I64], None),
+    "orc_gemv_f64_mt": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
     "orc_xorshift32_fill": ([ctypes.c_uint32, _P, ctypes.c_size_t], None),
     "orc_fixture_gemv": ([ctypes.c_uint32, _I64, _I64, _P, _P, _P], None),
     "orc_fixture_kind": ([ctypes.c_int, ctypes.c_uint32, _I64, _I64, _I64, _P, _P, _P], None),
@@ -158,11 +159,15 @@ def gemv_bf16(W, S, X, N: int, K: int, M: int = 1, nthreads: int = 1) -> np.ndar
     return Y
 
 
-def gemv_f64(W, S, X, N: int, K: int, M: int = 1):
-    """fp64 sum of the exact fp32 terms and the sum of their magnitudes."""
+def gemv_f64(W, S, X, N: int, K: int, M: int = 1, nthreads: int = 1):
+    """fp64 sum of the exact fp32 terms and the sum of their magnitudes
+    (rows split over `nthreads` threads; the values do not depend on it)."""
     Y = np.empty((M, N), np.float64)
     A = np.empty((M, N), np.float64)
-    _lib.orc_gemv_f64(_p(W), _p(S), _p(X), _p(Y), _p(A), N, K, M)
+    if nthreads > 1:
+        _lib.orc_gemv_f64_mt(_p(W), _p(S), _p(X), _p(Y), _p(A), N, K, M, nthreads)
+    else:
+        _lib.orc_gemv_f64(_p(W), _p(S), _p(X), _p(Y), _p(A), N, K, M)
     return Y, A
 
 
@@ -240,10 +245,24 @@ def bf16_ulp(v: np.ndarray) -> np.ndarray:
 CANCEL_FLOOR = 2.0 ** -16
 
 
-def check_tolerance(y_bits, W, S, X, N, K, M, ulps: float = 2.0):
+def check_against_reference_loop(y_bits, W, S, X, N, K, M, nthreads: int = 1, slack: int = 0):
+    """The W4A16 gate for the BASELINE workloads: (ok, stats, ref_stats).
+    ok iff y is within the check_tolerance bound and has at most `slack`
+    more outputs beyond 2 bf16 ulp of the fp64 value than the reference's
+    own fp32 CPU loop (ref_gemv_bf16) has on the same inputs. Those are
+    outputs whose terms cancel; the two accumulation orders round them
+    differently, so on one shape either side can have one more."""
+    r, a = gemv_f64(W, S, X, N, K, M, nthreads)
+    ok, st = check_tolerance_f64(y_bits, r, a, M, N)
+    _, sr = check_tolerance_f64(gemv_bf16(W, S, X, N, K, M, nthreads), r, a, M, N)
+    st["ref_max_ulp"], st["ref_n_over_2ulp"] = sr["max_ulp"], sr["n_over_2ulp"]
+    return ok and st["n_over_2ulp"] <= sr["n_over_2ulp"] + slack, st, sr
+
+
+def check_tolerance(y_bits, W, S, X, N, K, M, ulps: float = 2.0, nthreads: int = 1):
     """Pass iff |y - r| <= ulps * ulp_bf16(r) + CANCEL_FLOOR * sum|terms|,
     r = fp64 sum of the exact fp32 terms. Returns (ok, stats dict)."""
-    r, a = gemv_f64(W, S, X, N, K, M)
+    r, a = gemv_f64(W, S, X, N, K, M, nthreads)
     return check_tolerance_f64(y_bits, r, a, M, N, ulps)
 
 
@@ -291,8 +310,12 @@ def check_f16_tolerance(y_bits, W, S, X, N, K, M, ulps: float = 2.0):
     bad = ~(err <= tol) & ~big
     bad |= big & ~(np.isinf(y) & (np.sign(y) == np.sign(r)))
     ulp_dist = np.where(big, 0.0, err / fp16_ulp(r))
+    # the reference's own fp32 loop (ref_gemv) measured the same way, for scale
+    yr = fp16_to_f32(gemv_f16(W, S, X, N, K, M)).astype(np.float64)
+    ref_ulp = np.where(big, 0.0, np.abs(yr - r) / fp16_ulp(r))
     stats = {"max_ulp": float(ulp_dist.max()) if err.size else 0.0, "n_bad": int(bad.sum()),
-             "n_over_2ulp": int((ulp_dist > 2.0).sum()), "n": int(err.size)}
+             "n_over_2ulp": int((ulp_dist > 2.0).sum()), "n": int(err.size),
+             "ref_max_ulp": float(ref_ulp.max()) if err.size else 0.0}
     return not bad.any(), stats
 
 
@@ -366,6 +389,16 @@ def check_tolerance_f64(y_bits, r, a, M, N, ulps: float = 2.0):
 def check_bf16_tolerance(y_bits, W, X, N, K, M, ulps: float = 2.0):
     r, a = bf16_gemv_f64(W, X, N, K, M)
     return check_tolerance_f64(y_bits, r, a, M, N, ulps)
+
+
+def check_bf16_against_reference_loop(y_bits, W, X, N, K, M, nthreads: int = 1, slack: int = 0):
+    """check_against_reference_loop for the bf16 GEMV (ref_gemv_bf16 of
+    tests/cuda/test_bf16_gemv.cpp:62-73 as the reference loop)."""
+    r, a = bf16_gemv_f64(W, X, N, K, M)
+    ok, st = check_tolerance_f64(y_bits, r, a, M, N)
+    _, sr = check_tolerance_f64(bf16_gemv(W, X, N, K, M, nthreads), r, a, M, N)
+    st["ref_max_ulp"], st["ref_n_over_2ulp"] = sr["max_ulp"], sr["n_over_2ulp"]
+    return ok and st["n_over_2ulp"] <= sr["n_over_2ulp"] + slack, st, sr
 
 
 # ---- the reference's own comparator (oracle/_ref) ---------------------------

@@ -344,6 +344,54 @@ void orc_gemv_f64(const uint8_t* W, const uint16_t* S, const uint16_t* X,
   }
 }
 
+/* orc_gemv_f64 with the output rows n partitioned over threads (each
+ * output keeps its own sequential k loop, so the values are identical to
+ * the single-thread call). Test infrastructure for large traversals. */
+typedef struct {
+  const uint8_t* W;
+  const uint16_t* S;
+  const uint16_t* X;
+  double *Y, *Yabs;
+  int64_t N, K, M, n0, n1;
+} orc_f64_job;
+
+static void* orc_f64_run(void* p) {
+  orc_f64_job* j = (orc_f64_job*)p;
+  const int64_t G = j->K / 128, n = j->n1 - j->n0;
+  double* y = (double*)malloc(sizeof(double) * (size_t)(j->M * n));
+  double* a = (double*)malloc(sizeof(double) * (size_t)(j->M * n));
+  orc_gemv_f64(j->W + j->n0 * (j->K / 2), j->S + j->n0 * G, j->X, y, a, n, j->K, j->M);
+  for (int64_t m = 0; m < j->M; ++m)
+    for (int64_t r = 0; r < n; ++r) {
+      j->Y[m * j->N + j->n0 + r] = y[m * n + r];
+      if (j->Yabs) j->Yabs[m * j->N + j->n0 + r] = a[m * n + r];
+    }
+  free(y);
+  free(a);
+  return NULL;
+}
+
+void orc_gemv_f64_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X, double* Y,
+                     double* Yabs, int64_t N, int64_t K, int64_t M, int nthreads) {
+  if (nthreads <= 1 || N < 2) {
+    orc_gemv_f64(W, S, X, Y, Yabs, N, K, M);
+    return;
+  }
+  if (nthreads > 64) nthreads = 64;
+  pthread_t th[64];
+  orc_f64_job jobs[64];
+  const int64_t per = (N + nthreads - 1) / nthreads;
+  int used = 0;
+  for (int t = 0; t < nthreads; ++t) {
+    const int64_t n0 = t * per, n1 = n0 + per < N ? n0 + per : N;
+    if (n0 >= n1) break;
+    jobs[t] = (orc_f64_job){W, S, X, Y, Yabs, N, K, M, n0, n1};
+    pthread_create(&th[t], NULL, orc_f64_run, &jobs[t]);
+    ++used;
+  }
+  for (int t = 0; t < used; ++t) pthread_join(th[t], NULL);
+}
+
 /* ------------------------------------------------------------------------ */
 /* seeded fixtures                                                          */
 /* ------------------------------------------------------------------------ */

@@ -66,6 +66,8 @@ void orc_gemv_bf16_rows(const uint8_t* W, const uint16_t* S, const uint16_t* X,
 void orc_gemv_bf16_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X,
                       uint16_t* Y, int64_t N, int64_t K, int64_t M,
                       int nthreads);
+void orc_gemv_f64_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X, double* Y,
+                     double* Yabs, int64_t N, int64_t K, int64_t M, int nthreads);
 void orc_gemv_f64(const uint8_t* W, const uint16_t* S, const uint16_t* X,
                   double* Y, double* Yabs, int64_t N, int64_t K, int64_t M);
 

@@ -140,10 +140,12 @@ def test_lm_head_synthetic_batch8(w4, orc, dev):
     W = orc.f32_to_bf16(orc.synth_normal(0xC0DA, 0.02, N * K)).reshape(N, K)
     X = orc.synth_act(0xAC7, M, K)
     Y = run(w4, *up(dev, W, X), N, K, M)
-    ok, st = orc.check_bf16_tolerance(Y, W, X, N, K, M)
+    # every output within the bound, and over these 2M outputs no more beyond
+    # 2 ulp than the reference's own CPU loop (ref_gemv_bf16) has
+    ok, st, _ = orc.check_bf16_against_reference_loop(Y, W, X, N, K, M,
+                                                     max(1, min(16, __import__("os").cpu_count() or 1)))
     print(f"  lm_head M=8: {st}", flush=True)
     assert ok, st
-    assert st["n_over_2ulp"] <= st["n"] // 10000
 
 
 def test_cpp_reference_names(w4, orc, dev):

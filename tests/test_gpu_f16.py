@@ -5,7 +5,9 @@ zero-group and misaligned cases (test_int4_gemv.cpp:115-290), plus row
 parity and layout bit-identity.
 
 Bar: |y - r| <= 2 ulp_fp16(r) + 2^-16 sum|terms| (oracle.check_f16_tolerance)
-and the reference's compare_fp16_stages where oracle/_ref is built."""
+and the reference's compare_fp16_stages where oracle/_ref is built. On the
+reference's own fixtures no output may be more than 2 fp16 ulp from the
+fp64 value (the floor term is for cancellation-heavy synthetic inputs)."""
 import numpy as np
 import pytest
 import torch
@@ -25,13 +27,16 @@ def down(t):
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def check(orc, Y, W, S, X, N, K, M, label):
+def check(orc, Y, W, S, X, N, K, M, label, strict=False):
     ok, st = orc.check_f16_tolerance(Y, W, S, X, N, K, M)
     print(f"  {label} N={N} K={K} M={M}: {st}", flush=True)
     assert ok, (label, st)
+    if strict:
+        assert st["n_over_2ulp"] == 0, (label, st)
     if orc.ref is not None:
         ok, mx, idx = orc.ref.compare_fp16_stages(orc.gemv_f16(W, S, X, N, K, M), Y)
         assert ok, (label, mx, idx)
+    return st
 
 
 SHAPES = [(1024, 1024), (512, 1024), (2816, 1024), (1024, 2816), (1005, 1024), (1, 128)]
@@ -45,7 +50,7 @@ def test_reference_shapes(w4, orc, dev, i):
     y = torch.empty(N, dtype=torch.float16, device=dev)
     w4.int4_gemv(w, s, x[0], y, N, K)
     Y = down(y).reshape(1, N)
-    check(orc, Y, W, S, X, N, K, 1, "int4_gemv")
+    check(orc, Y, W, S, X, N, K, 1, "int4_gemv", strict=True)
     p = w4.repack(w, s, N, K)
     assert np.array_equal(down(w4.gemv_f16_prepacked(p, x, N, K)).reshape(1, N), Y)
 
@@ -73,7 +78,7 @@ def test_misaligned_bases(w4, orc, dev):
     assert lib.cudalm_w4a16_gemv_f16(wb.data_ptr() + 8, s.data_ptr(), xb.data_ptr() + 4,
                                      y.data_ptr(), N, K, 1, st) == 0
     Ym = down(y).reshape(1, N)
-    check(orc, Ym, W, S, X, N, K, 1, "misaligned")
+    check(orc, Ym, W, S, X, N, K, 1, "misaligned", strict=True)
     Ya = down(w4.gemv_f16(w, s, x, N, K)).reshape(1, N)
     if orc.ref is not None:
         ok, mx, _ = orc.ref.compare_fp16_stages(Ya, Ym)

@@ -55,6 +55,21 @@ def run(w4, w, s, x, N, K, M, variant="auto"):
     return down(y).reshape(M, N)
 
 
+THREADS = max(1, min(16, __import__("os").cpu_count() or 1))  # the GPU box's host share
+
+
+def assert_baseline(orc, Y, W, S, X, N, K, M, label=""):
+    """BASELINE workloads: every output within the bound; the count beyond
+    2 ulp is printed beside the reference CPU loop's on the same inputs.
+    (Per shape these are a handful of cancelled sums either way; the gate
+    that the kernels have no more of them than the loop is taken over whole
+    census traversals, tests/test_gpu_census.py.)"""
+    _, st, _ = orc.check_against_reference_loop(Y, W, S, X, N, K, M, THREADS)
+    print(f"  {label} N={N} K={K} M={M}: {st}", flush=True)
+    assert st["n_bad"] == 0, (label, st)
+    return st
+
+
 def assert_tol(orc, Y, W, S, X, N, K, M, label=""):
     ok, st = orc.check_tolerance(Y, W, S, X, N, K, M)
     print(f"  {label} N={N} K={K} M={M}: {st}", flush=True)
@@ -160,9 +175,12 @@ def test_parity_gate_small(w4, orc, dev, N, K, kind):
 
 
 @pytest.mark.parametrize("N,K", CENSUS[2:])
-@pytest.mark.parametrize("kind", ["random", "boundary", "mixed_sign"])
+@pytest.mark.parametrize("kind", ["random", "zero", "small", "mixed_sign", "boundary"])
 def test_parity_gate_census(w4, orc, dev, N, K, kind):
-    _parity_case(w4, orc, dev, N, K, 3, kind, 0x1234ABCD)
+    # test_w4a16_qwen35_optimized.cpp:154-171,456: every census shape x the
+    # four reference seeds x the five input classes
+    for seed in orc.REFERENCE_SEEDS:
+        _parity_case(w4, orc, dev, N, K, 3, kind, seed)
 
 
 # ---------------------------------------------------------------- BASELINE workloads ---
@@ -175,8 +193,7 @@ def test_census_synthetic(w4, orc, dev, N, K, M):
     W, S = orc.synth_w4a16(0xC0DA0000 + N + K, N, K)
     X = orc.synth_act(0xAC7 + M, M, K)
     Y = run(w4, *up(dev, W, S, X), N, K, M)
-    st = assert_tol(orc, Y, W, S, X, N, K, M, "census")
-    assert st["n_over_2ulp"] <= max(1, st["n"] // 10000)
+    assert_baseline(orc, Y, W, S, X, N, K, M, "census")
 
 
 @pytest.mark.parametrize("N,K", [(3584, 1024), (1024, 3584), (16, 1024), (6144, 1024)])
@@ -187,7 +204,7 @@ def test_prefill_chunks(w4, orc, dev, N, K, M):
     X = orc.synth_act(0xF00D + M, M, K)
     w, s, x = up(dev, W, S, X)
     Y = run(w4, w, s, x, N, K, M)
-    assert_tol(orc, Y, W, S, X, N, K, M, "prefill")
+    assert_baseline(orc, Y, W, S, X, N, K, M, "prefill")
     for b in (0, 17, M - 1):
         assert np.array_equal(Y[b], run(w4, w, s, x[b:b + 1], N, K, 1)[0]), b
 
@@ -221,8 +238,7 @@ def test_lm_head_full_size(w4, orc, dev):
     X = orc.synth_act(0x11AE, 1, K)
     w, s, x = up(dev, W, S, X)
     Y = run(w4, w, s, x, N, K, 1)
-    st = assert_tol(orc, Y, W, S, X, N, K, 1, "lm_head")
-    assert st["n_over_2ulp"] <= N // 10000
+    assert_baseline(orc, Y, W, S, X, N, K, 1, "lm_head")
     p = w4.repack(w, s, N, K)
     yp = w4.gemv_prepacked(p, x, N, K, 1)
     assert np.array_equal(down(yp).reshape(1, N), Y)
@@ -262,8 +278,7 @@ def test_large_n_small_m(w4, orc, dev, N, M):
     X = orc.synth_act(0x7A12 + M, M, K)
     w, s, x = up(dev, W, S, X)
     Y = run(w4, w, s, x, N, K, M)
-    st = assert_tol(orc, Y, W, S, X, N, K, M, "large_n")
-    assert st["n_over_2ulp"] <= max(1, st["n"] // 10000)
+    assert_baseline(orc, Y, W, S, X, N, K, M, "large_n")
     p = w4.repack(w, s, N, K)
     yp = w4.gemv_prepacked(p, x, N, K, M)
     assert np.array_equal(down(yp).reshape(M, N), Y)
@@ -397,8 +412,9 @@ def test_piece_split_equals_stream(w4, orc, dev, N, K, M):
 @pytest.mark.parametrize("seed", range(6))
 def test_random_shapes_auto_equals_tile(w4, orc, dev, seed):
     # seeded random shapes across the dispatch plans (piece split of every
-    # plan, unit split, stream, prefill GEMM, 16-row passes): the auto path,
-    # file layout and prepacked, against the tile kernel, bit for bit
+    # plan, unit split, stream, prefill GEMM, 16-row passes): the tile
+    # kernel within tolerance of the oracle, and the auto path, file layout
+    # and prepacked bit for bit equal to it
     rng = np.random.default_rng(0xD15 + seed)
     for _ in range(6):
         K = 128 * int(rng.integers(1, 33))
@@ -408,6 +424,8 @@ def test_random_shapes_auto_equals_tile(w4, orc, dev, seed):
         X = orc.synth_act(int(rng.integers(1 << 30)), M, K)
         w, s, x = up(dev, W, S, X)
         ref = run(w4, w, s, x, N, K, M, "tile16")
+        # the shared decode / offset / epilogue code itself, against the oracle
+        assert_tol(orc, ref, W, S, X, N, K, M, "random")
         got = run(w4, w, s, x, N, K, M)
         assert np.array_equal(got, ref), ("auto", N, K, M)
         p = w4.repack(w, s, N, K)
