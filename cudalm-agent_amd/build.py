@@ -88,7 +88,31 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("hipcc failed linking libcudalm_w4a16.so")
     os.replace(tmp, LIB)
+    build_boundary_check(verbose)
     return LIB
+
+
+CHECK_SRC = os.path.join(REPO, "tests", "cpp", "boundary_check.cpp")
+CHECK_BIN = os.path.join(REPO, "tests", "cpp", "boundary_check")
+
+
+def build_boundary_check(verbose: bool = False) -> str:
+    """The reference-side C++ caller used by tests/test_gpu_cpp_boundary.py:
+    compiled against include/cudalm/ and linked with the library (rpath to
+    the package directory)."""
+    rpath = "$ORIGIN/" + os.path.relpath(os.path.dirname(LIB), os.path.dirname(CHECK_BIN))
+    cmd = [hipcc(), "--offload-arch=gfx950", "-O2", "-std=c++17",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-Wno-unused-command-line-argument", "-I", os.path.join(REPO, "include"), CHECK_SRC,
+           "-L", os.path.dirname(LIB), "-lcudalm_w4a16", f"-Wl,-rpath,{rpath}", "-o", CHECK_BIN + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed building tests/cpp/boundary_check")
+    os.replace(CHECK_BIN + ".tmp", CHECK_BIN)
+    return CHECK_BIN
 
 
 if __name__ == "__main__":
