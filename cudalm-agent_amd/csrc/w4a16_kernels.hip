@@ -887,6 +887,16 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
 // SwiGLU; P holds gate then up with equal N, row tile t is gate tile t and
 // up tile nt + t, and the output is silu(gate) * up on the bf16-rounded
 // projections (blockIdx.y walks chunks of mc activation rows).
+#ifdef CUDALM_SPLIT_PROBE
+// measurement build only: per-wave phase timestamps (s_memrealtime, 100 MHz)
+__device__ unsigned long long g_split_probe[4096 * 16 * 8];
+#define SPLIT_PROBE(k)                                                         \
+  if (lane == 0 && blockIdx.x < 4096 && blockIdx.y == 0)                       \
+  g_split_probe[(blockIdx.x * 16 + wave) * 8 + (k)] = __builtin_amdgcn_s_memrealtime()
+#else
+#define SPLIT_PROBE(k)
+#endif
+
 template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, int NP = 1,
           bool DX = false, class PT = ProjTable>
 __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
@@ -898,6 +908,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   const int i = lane & 15, a = lane >> 4;
+  SPLIT_PROBE(0);
   const int nt = NP == 1 ? P.ntiles : P.tile_end[0];  // row tiles
   const int U = (G + kUnit - 1) / kUnit;
   const int H = (G + HG - 1) / HG;  // pieces of a tile that hold groups
@@ -935,6 +946,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
                                                G, h * HG);
   };
   load_slot(min(wave, nslots - 1));
+  SPLIT_PROBE(1);
   const u32x4_t* xrow[CT];
   const float* corr = nullptr;
   if constexpr (!DX) corr = stream_prologue<CT, Act, true>(xs, xrow, Xc, K, mrows, wave, i, a, sb0);
@@ -988,7 +1000,9 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
       }
     }
   }
+  SPLIT_PROBE(2);
   __syncthreads();
+  SPLIT_PROBE(3);
   if (wave < TPR && t0 + wave < nt) {
     f32x4_t total[NP][CT];
 #pragma unroll
@@ -997,28 +1011,41 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) total[pj][ct] = zero;
       for (int u = 0; u < U; ++u) {
+        // every parked tmp and scale of the unit first (the reads go out
+        // together), then the fma chain in group order
+        constexpr int NPK = (PPU - 1) * HG;
         f32x4_t p[CT];
+        f32x4_t tv[NPK > 0 ? NPK : 1][CT];
+        float sv[NPK > 0 ? NPK : 1];
+        const int gbase = u * PPU * HG;  // first group of the unit
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) p[ct] = heads[((tu * U + u) * CT + ct) * 64 + lane];
-        for (int pp = 1; pp < PPU; ++pp) {
-          const int base = ((tu * U + u) * (PPU - 1) + pp - 1) * HG;
-          const int g0 = (u * PPU + pp) * HG;
-          for (int gg = 0; gg < HG && g0 + gg < G; ++gg) {
-            const float sc = scs[(base + gg) * 16 + i];
 #pragma unroll
-            for (int ct = 0; ct < CT; ++ct) {
-              const f32x4_t t = tmps[((base + gg) * CT + ct) * 64 + lane];
+        for (int q = 0; q < NPK; ++q) {
+          const int base = (tu * U + u) * NPK + q;
+          if (gbase + HG + q < G) {
+            sv[q] = scs[base * 16 + i];
 #pragma unroll
-              for (int r = 0; r < NR; ++r) p[ct][r] = __builtin_fmaf(sc, t[r], p[ct][r]);
-            }
+            for (int ct = 0; ct < CT; ++ct) tv[q][ct] = tmps[(base * CT + ct) * 64 + lane];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < NPK; ++q) {
+          if (gbase + HG + q < G) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+              for (int r = 0; r < NR; ++r) p[ct][r] = __builtin_fmaf(sv[q], tv[q][ct][r], p[ct][r]);
           }
         }
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) total[pj][ct] = total[pj][ct] + p[ct];
       }
     }
+    SPLIT_PROBE(4);
     if constexpr (NP == 1) {
       store_tile<NR, CT, Act, PT>(P, t0 + wave, total[0], M, i, a);
+      SPLIT_PROBE(5);
     } else {
       const int N = P.n[0];
       const int n = (t0 + wave) * kTileRows + i;
@@ -2109,6 +2136,12 @@ int f16_dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_
 }
 
 }  // namespace
+
+#ifdef CUDALM_SPLIT_PROBE
+extern "C" int cudalm_split_probe_read(void* host, size_t bytes) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_split_probe), bytes) == hipSuccess ? 0 : -1;
+}
+#endif
 
 extern "C" {
 
