@@ -170,7 +170,13 @@ def time_launches(torch, launches, reps: int, warmup: int, stream):
 
 def stream_time(torch, launches, reps: int, warmup: int, stream):
     """Seconds per launch: `reps` launches back to back (round-robin over
-    `launches`) between two HIP events on `stream`, after `warmup`."""
+    `launches`) between two HIP events on `stream`, after `warmup`.
+
+    The window holds the host's launch loop: when the host enqueues slower
+    than the GPU drains, the GPU waits between launches and the figure rises
+    (1.5-4 us on ~25 us kernels after a pass that created many objects, or
+    after the CPU idled), while the kernel trace shows the same kernel
+    duration and HBM bytes. Callers take the median of several windows."""
     for i in range(warmup):
         launches[i % len(launches)]()
     torch.cuda.synchronize()
