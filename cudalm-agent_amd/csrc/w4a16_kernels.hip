@@ -711,6 +711,114 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
 // partials of those tiles side by side, park them in LDS, and the unit
 // partials of each tile are summed in unit order. Same bits as the stream
 // kernel; shorter latency when tiles alone cannot fill the machine.
+// Pair stream kernel (single projection, two column tiles, M = 17..32):
+// as the piece stream kernel, but each wave streams two adjacent 16-row
+// weight tiles together, so every activation fragment and offset seed it
+// reads from LDS feeds the MFMAs of both tiles. At M = 32 the one-tile
+// kernel reads 64 KB of activation operands from LDS per weight tile, which
+// makes the LM head LDS-bound (~92 B/clk per CU) on top of its HBM stream;
+// pairs halve that. The per-output operation sequence is unchanged.
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, bool FULL, int WV, class PT>
+__global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_kernel(
+    const PT P, const uint16_t* __restrict__ X, int K, int M) {
+  extern __shared__ u32x4_t xs[];
+  constexpr int PPU = kUnit / HG;  // pieces per 8-group unit
+  const int G = K >> 7;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int i = lane & 15, a = lane >> 4;
+  const int H = (G + HG - 1) / HG;  // pieces per tile
+  const int ntiles = P.ntiles;
+  const int npairs = (ntiles + 1) >> 1;
+  const int stride = static_cast<int>(gridDim.x) * WV;
+  int p = static_cast<int>(blockIdx.x) * WV + wave;
+  const bool active = p < npairs;
+
+  StageBatch sb0;
+  stage_load(sb0, X, K, 0, M, 0, K, 0);
+  StreamPiece<HG> cur[2], nxt[2];
+  TileAddr acur[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    acur[k] = tile_addr<PACKED>(P, K, G, min(2 * min(p, npairs - 1) + k, ntiles - 1), lane);
+    stream_load_piece<HG, PACKED, SVEC, FULL>(cur[k], acur[k], G, 0);
+  }
+  const u32x4_t* xrow[CT];
+  const float* corr = stream_prologue<CT, Act, false>(xs, xrow, X, K, M, wave, i, a, sb0);
+  if (!active) return;
+
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t part[2][CT], total[2][CT];
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) part[k][ct] = total[k][ct] = zero;
+  int h = 0;
+  while (true) {
+    int np = p, nh = h + 1;
+    if (nh == H) {
+      nh = 0;
+      np = p + stride;
+    }
+    const bool has_next = np < npairs;
+    TileAddr anx[2] = {acur[0], acur[1]};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      if (has_next && nh == 0) anx[k] = tile_addr<PACKED>(P, K, G, min(2 * np + k, ntiles - 1), lane);
+      // past the last piece, load from the sink instead of branching around the loads
+      if (!has_next) anx[k].w = g_piece_sink + lane * 16;
+      stream_load_piece<HG, PACKED, SVEC, FULL>(nxt[k], anx[k], G, (has_next ? nh : 0) * HG);
+    }
+    const int g0 = h * HG;
+    using L = Layout<Act, PACKED>;
+#pragma unroll
+    for (int gg = 0; gg < HG; ++gg) {
+      if (FULL || gg < G - g0) {
+        const int g = g0 + gg;
+        u32x4_t xa[CT][4];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) load_group_x(xa[ct], xrow[ct] + g * 16, a);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          f32x4_t t[CT];
+          group_tmp_x<NR, CT, L, false>(t, xa, cur[k].w[gg], corr + g * 16 * CT, a);
+          const float sc = half_bits_to_f32((cur[k].s[gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int r = 0; r < NR; ++r) part[k][ct][r] = __builtin_fmaf(sc, t[ct][r], part[k][ct][r]);
+        }
+      }
+    }
+    // an 8-group unit ends after its last piece or at the tile's last piece
+    if ((h % PPU) == PPU - 1 || h == H - 1) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          total[k][ct] = total[k][ct] + part[k][ct];
+          part[k][ct] = zero;
+        }
+    }
+    if (h == H - 1) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        if (2 * p + k < ntiles) store_tile<NR, CT, Act, PT>(P, 2 * p + k, total[k], M, i, a);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) total[k][ct] = zero;
+      }
+    }
+    if (!has_next) break;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      cur[k] = nxt[k];
+      acur[k] = anx[k];
+    }
+    p = np;
+    h = nh;
+  }
+}
+
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, class PT = ProjTable>
 __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
     const PT P, const uint16_t* __restrict__ X, int K, int M) {
@@ -1628,6 +1736,18 @@ int proj_one_enabled() {
 }
 
 // Workgroups per CU of the 8-wave stream kernel (two column tiles).
+// Waves per workgroup of the pair stream kernel (0 = off), and resident
+// workgroups per CU (measurement overrides).
+int stream_pair_waves() {
+  static const int v = env_setting("CUDALM_W4A16_STREAM_PAIR", 8, 0, 8);
+  return v == 4 || v == 8 ? v : 0;
+}
+
+int stream_pair_wgs_per_cu() {
+  static const int v = env_setting("CUDALM_W4A16_STREAM_PAIR_WGS_PER_CU", 1, 1, 4);
+  return v;
+}
+
 int stream_occupancy_wide() {
   static const int occ = env_setting("CUDALM_W4A16_STREAM_WIDE_WGS_PER_CU", 2, 1, 8);
   return occ;
@@ -1678,6 +1798,29 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   // 4.30 -> 4.10 us); waves that stream many tiles share the table (inline
   // chains cost the LM head 0.9 us at M = 1 and 3.6 us at M = 8).
   const bool ioff = t_static == ntiles && ntiles <= pwg * WV;
+  // two column tiles of one projection: the pair kernel (CUDALM_W4A16_STREAM_PAIR,
+  // 1 = on, the default; 0 = the one-tile kernel, for measurement)
+  if constexpr (CT == 2) {
+    if (P.count == 1 && proj_one_enabled() && stream_pair_waves() > 0 && mode == 1) {
+      const ProjOne one = shrink_table<1>(P);
+      const int wv = stream_pair_waves();
+      const int npairs = (ntiles + 1) / 2;
+      auto launch_pair = [&](auto kern, int WVv) {
+        if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+        const int fit = lds_fit > 0 ? lds_fit : 1;
+        const int cap = cu_count() * (fit < stream_pair_wgs_per_cu() ? fit : stream_pair_wgs_per_cu());
+        const int want = (npairs + WVv - 1) / WVv;
+        hipLaunchKernelGGL(kern, dim3(want < cap ? want : cap), dim3(WVv * 64), lds, stream, one, X,
+                           K, M);
+        return launch_status();
+      };
+      if (wv == 4)
+        return G % 4 == 0 ? launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, true, 4, ProjOne>, 4)
+                          : launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, false, 4, ProjOne>, 4);
+      return G % 4 == 0 ? launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, true, 8, ProjOne>, 8)
+                        : launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, false, 8, ProjOne>, 8);
+    }
+  }
   auto go = [&](const auto& T) {
     using PT = std::decay_t<decltype(T)>;
     auto kern =
