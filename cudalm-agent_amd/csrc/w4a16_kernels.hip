@@ -1343,6 +1343,15 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
   const int tid = static_cast<int>(threadIdx.x) - slice * NT;
   const int i = lane & 15, a = lane >> 4;
   const int m0 = blockIdx.y * TM;
+#ifdef CUDALM_SPLIT_PROBE
+  const int wave_p = wave_id();
+#define UNIT_PROBE(k)                                                                  \
+  if (lane == 0 && blockIdx.x < 256 && blockIdx.y < 16 && wave_p < 16)                 \
+  g_split_probe[((blockIdx.y * 256 + blockIdx.x) * 16 + wave_p) * 8 + (k)] = __builtin_amdgcn_s_memrealtime()
+#else
+#define UNIT_PROBE(k)
+#endif
+  UNIT_PROBE(0);
   const int mrows = min(TM, M - m0);
   u32x4_t* xs = lds + slice * XB;
   float* corr = reinterpret_cast<float*>(lds + KS * XB) + slice * (kUnit * CT * 16);
@@ -1408,6 +1417,7 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
     }
     // the unit's activations, rows clamped to the last valid one
     if (it > 0) __syncthreads();  // previous unit's readers are done
+    UNIT_PROBE(1);
     {
       // thread tid stages block b = tid % 128 of rows tid / 128 + q * RS
       constexpr int RS = NT / (kUnit * 16);
@@ -1425,6 +1435,7 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
       for (int q = 0; q < BPT; ++q) xdst[q * RS * PB] = pair_order(v[q]);
     }
     __syncthreads();
+    UNIT_PROBE(2);
     // offset table of the unit: chains (group, column tile) split over waves
     // (IOFF: each wave runs the chains of its own groups inline instead, the
     // same operands, and the table and its barrier are skipped)
@@ -1438,6 +1449,7 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
       }
       __syncthreads();
     }
+    UNIT_PROBE(3);
     if (!any_ok) continue;
 
     f32x4_t part[RB][CT];
@@ -1490,6 +1502,7 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) acc[0][rb][ct] = acc[0][rb][ct] + part[rb][ct];
+      UNIT_PROBE(4);
     } else {
 #pragma unroll
       for (int q = 0; q < NPART; ++q)
@@ -1548,6 +1561,7 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
           col[static_cast<size_t>(ct * 16 + r) * N] =
               static_cast<uint16_t>(f32_to_bf16_rne(16.0f * total[rb][ct][r]));
   }
+  UNIT_PROBE(5);
 }
 
 // ---------------------------------------------------------------------------

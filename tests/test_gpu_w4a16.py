@@ -196,7 +196,7 @@ def test_census_synthetic(w4, orc, dev, N, K, M):
     assert_baseline(orc, Y, W, S, X, N, K, M, "census")
 
 
-@pytest.mark.parametrize("N,K", [(3584, 1024), (1024, 3584), (16, 1024), (6144, 1024)])
+@pytest.mark.parametrize("N,K", CENSUS)
 @pytest.mark.parametrize("M", [64, 100, 512])
 def test_prefill_chunks(w4, orc, dev, N, K, M):
     # M-token prefill chunk GEMM
