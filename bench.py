@@ -251,6 +251,8 @@ def main():
                     help="headline workload only (for counter collection)")
     ap.add_argument("--bf16-lm-head-only", action="store_true",
                     help="only the tied bf16 LM head lines (for counter collection)")
+    ap.add_argument("--cfg0-mib", type=int, default=2048,
+                    help="MiB of weight copies the configs[0] line rotates over (profiler runs: 320)")
     ap.add_argument("--only", default="", choices=["", "config0", "lm_head_m8", "lm_head_m32"],
                     help="kernel-trace / counter run: the headline, then only this side line")
     ap.add_argument("--census-mode", default="", metavar="KEY",
@@ -368,9 +370,9 @@ def main():
     file_gbs = nbytes / file_per / 1e9 if file_per == file_per else None
 
     # M = 1, N = 3584, K = 1024. The launches rotate over 2 GiB
-    # of weight copies (1,130 matrices of 1.9 MB: 16 synthesized ones, each
-    # at ~70 addresses), more than the 256 MB MALL, so every launch reads
-    # its weights from HBM as it would in the census.
+    # of weight copies by default (1,130 matrices of 1.9 MB: 16 synthesized
+    # ones, each at ~70 addresses), more than the 256 MB MALL, so every
+    # launch reads its weights from HBM as it would in the census.
     cfg0_s = None
     if not args.lm_head_only and not args.census_mode and args.only in ("", "config0"):
         N0, K0 = 3584, 1024
@@ -378,14 +380,15 @@ def main():
         for c in range(16):
             w, s = synth_weights(torch, N0, K0, 0x3584 + c, dev)
             base.append(w4.repack(w, s, N0, K0))
-        ncopies = -(-(2 << 30) // base[0].numel())
+        ncopies = max(16, -(-(args.cfg0_mib << 20) // base[0].numel()))
         c0 = [base[c % 16] if c < 16 else base[c % 16].clone() for c in range(ncopies)]
         x0 = synth_act(torch, 1, K0, 0x3585, dev)
         y0 = torch.empty((1, N0), dtype=torch.bfloat16, device=dev)
         x0p, y0p = x0.data_ptr(), y0.data_ptr()
         c0_launch = [(lambda pp=p.data_ptr(): lib.cudalm_w4a16_gemv_bf16_prepacked(pp, x0p, y0p, N0, K0, 1, sraw))
                      for p in c0]
-        cfg0_s = graph_time(torch, lambda: [f() for f in c0_launch], 20, stream) / len(c0_launch)
+        cfg0_s = graph_time(torch, lambda: [f() for f in c0_launch], 20 if len(c0_launch) <= 200 else 5,
+                            stream) / len(c0_launch)
         del c0, base
 
     # ---------------- census: 186 projections + LM head per decode step ----------------
@@ -445,15 +448,15 @@ def main():
                 }
                 prof = census_kernel_sum_us(key)
                 if prof:
-                    # census roofline: summed kernel durations against the graph
-                    # wall of the same traversal, both from the committed
-                    # rocprofv3 kernel trace (the tracer lengthens every dispatch,
-                    # so the ratio is taken within the traced run)
-                    ksum, twall = prof
+                    # census roofline: the summed kernel durations of one
+                    # traversal (committed rocprofv3 kernel trace) against this
+                    # run's untraced graph wall; a ratio near or above 1 means
+                    # the kernels themselves fill the traversal (the tracer
+                    # lengthens each dispatch, and its wall depends on the box)
+                    ksum = prof[0]
                     census[key].update({
                         "sum_kernel_us_traced": ksum,
-                        "graph_wall_us_traced": twall,
-                        "kernel_fraction_of_wall_traced": round(ksum / twall, 3),
+                        "sum_kernel_over_wall": round(ksum * 1e-6 / t, 3),
                         "GBps_over_sum_kernel": round(tot_bytes / (ksum * 1e-6) / 1e9, 1),
                         "frac_hbm_peak_over_sum_kernel": round(tot_bytes / (ksum * 1e-6) / 1e9
                                                                / HBM_PEAK_GBS, 4),
