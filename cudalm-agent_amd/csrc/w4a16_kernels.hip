@@ -1394,7 +1394,21 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
     const int uc = min(u, U - 1);  // a slice past the last unit re-reads it and skips the math
     const int g0 = uc * kUnit;
     const int gn = u < U ? min(kUnit, G - g0) : 0;
-    // this unit's weights and scales (group indices clamped to G - 1)
+    // the unit's activations first: they are staged and feed the offset
+    // table before any weight is used, and loads return in issue order
+    constexpr int RS = NT / (kUnit * 16);
+    static_assert(NT % (kUnit * 16) == 0, "a thread keeps one block column");
+    const int b = tid & (kUnit * 16 - 1);  // thread tid stages block b of rows tid / 128 + q * RS
+    const int r0 = tid / (kUnit * 16);
+    u32x4_t v[BPT];
+    {
+      const uint16_t* xcol = X + static_cast<size_t>(m0) * K + min(g0 * kGroup + 8 * b, K - 8);
+#pragma unroll
+      for (int q = 0; q < BPT; ++q)
+        v[q] = *reinterpret_cast<const u32x4_t*>(
+            xcol + static_cast<size_t>(min(r0 + q * RS, mrows - 1)) * K);
+    }
+    // then this unit's weights and scales (group indices clamped to G - 1)
     u32x4_t w[RB][kUnit];
     uint32_t sc[RB][kUnit / 2];
 #pragma unroll
@@ -1415,21 +1429,9 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
                       (static_cast<uint32_t>(srow[min(g0 + 2 * q + 1, G - 1)]) << 16);
       }
     }
-    // the unit's activations, rows clamped to the last valid one
     if (it > 0) __syncthreads();  // previous unit's readers are done
     UNIT_PROBE(1);
     {
-      // thread tid stages block b = tid % 128 of rows tid / 128 + q * RS
-      constexpr int RS = NT / (kUnit * 16);
-      static_assert(NT % (kUnit * 16) == 0, "a thread keeps one block column");
-      const int b = tid & (kUnit * 16 - 1);
-      const int r0 = tid / (kUnit * 16);
-      const uint16_t* xcol = X + static_cast<size_t>(m0) * K + min(g0 * kGroup + 8 * b, K - 8);
-      u32x4_t v[BPT];
-#pragma unroll
-      for (int q = 0; q < BPT; ++q)
-        v[q] = *reinterpret_cast<const u32x4_t*>(
-            xcol + static_cast<size_t>(min(r0 + q * RS, mrows - 1)) * K);
       u32x4_t* xdst = xs + r0 * PB + b;
 #pragma unroll
       for (int q = 0; q < BPT; ++q) xdst[q * RS * PB] = pair_order(v[q]);
