@@ -657,9 +657,9 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
   // x's first batch, then the first piece's weights, fly together
   StageBatch sb0;
   stage_load(sb0, X, K, 0, M, 0, K, 0);
-  StreamPiece<HG> cur, nxt;
+  StreamPiece<HG> bufA, bufB;
   TileAddr acur = tile_addr<PACKED>(P, K, G, min(t, ntiles - 1), lane);
-  stream_load_piece<HG, PACKED, SVEC, FULL>(cur, acur, G, 0);
+  stream_load_piece<HG, PACKED, SVEC, FULL>(bufA, acur, G, 0);
   const u32x4_t* xrow[CT];
   const float* corr = stream_prologue<CT, Act, IOFF>(xs, xrow, X, K, M, wave, i, a, sb0);
   if (!active) return;
@@ -668,8 +668,21 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
   f32x4_t part[CT], total[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) part[ct] = total[ct] = zero;
+  // the finished tile's sums, stored at the next step (after its wait)
+  f32x4_t done[CT];
+  int done_t = -1;
   int h = 0;
-  while (true) {
+  // One piece. Loads and stores share one in-order memory counter: the
+  // step waits for all of its memory operations first (the current piece),
+  // then stores the tile finished in the previous step, then issues the
+  // next piece's loads, so no wait ever covers a store issued just before
+  // it. The two piece buffers alternate (two steps per loop turn).
+  auto step = [&](const StreamPiece<HG>& cur, StreamPiece<HG>& nxt) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt at their maxima
+    if (done_t >= 0) {
+      store_tile<NR, CT, Act, PT>(P, done_t, done, M, i, a);
+      done_t = -1;
+    }
     int nt = t, nh = h + 1;
     if (nh == H) {
       nh = 0;
@@ -694,16 +707,21 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
       }
     }
     if (h == H - 1) {
-      store_tile<NR, CT, Act, PT>(P, t, total, M, i, a);
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
+      for (int ct = 0; ct < CT; ++ct) {
+        done[ct] = total[ct];
+        total[ct] = zero;
+      }
+      done_t = t;
     }
-    if (!has_next) break;
-    cur = nxt;
     acur = anx;
     t = nt;
     h = nh;
+    return has_next;
+  };
+  while (step(bufA, bufB) && step(bufB, bufA)) {
   }
+  if (done_t >= 0) store_tile<NR, CT, Act, PT>(P, done_t, done, M, i, a);
 }
 
 // Split kernel: few weight tiles, several units per tile (K >= 2048). A
