@@ -837,6 +837,185 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_kernel(
   }
 }
 
+// Write-only target of the counted pair kernel's first stores (no pair is
+// finished yet, but the step issues its 16 stores so that the number of
+// memory operations per step is fixed). Nothing reads it.
+__device__ __align__(256) uint16_t g_store_sink[64];
+
+// s_waitcnt vmcnt(v), expcnt and lgkmcnt at their maxima, for the counts
+// the counted kernel uses (v is a constant once the caller is unrolled).
+constexpr int vm_wait(int v) { return (v & 15) | ((v >> 4) << 14) | 0x0F70; }
+__device__ __forceinline__ void wait_vm_after(int v) {
+  switch (v) {
+#define CUDALM_VM_CASE(n) \
+  case n:                 \
+    __builtin_amdgcn_s_waitcnt(vm_wait(n)); \
+    break;
+    CUDALM_VM_CASE(10) CUDALM_VM_CASE(12) CUDALM_VM_CASE(14) CUDALM_VM_CASE(16)
+    CUDALM_VM_CASE(26) CUDALM_VM_CASE(28) CUDALM_VM_CASE(30) CUDALM_VM_CASE(32)
+#undef CUDALM_VM_CASE
+    default:
+      __builtin_amdgcn_s_waitcnt(vm_wait(0));
+  }
+}
+
+// Counted pair kernel: the pair stream kernel's work and per-output
+// operation sequence for one prepacked projection with K = 1024 (a tile is
+// two pieces of 4 groups), M = 32 and N % 32 == 0 (every output of a pair
+// exists), with the waits for its loads placed by the kernel. Loads and
+// stores share one in-order memory counter, and the compiler's own waits,
+// which must hold on every path through the loop, also wait for stores
+// issued after the loads they need. Here the loop body is one tile pair in
+// two steps with fixed memory operations:
+//   step 0: the previous pair's 16 output stores (the first pass stores
+//           to a sink), the loads of piece 1 (10: both
+//           tiles' scales, then their group slabs group by group), then
+//           piece 0's groups;
+//   step 1: the loads of the next pair's piece 0 (the sink's weights past
+//           the last pair), then piece 1's groups.
+// Each group waits for exactly the operations issued before its slabs, so
+// the stores overlap a step of loads and compute, and a group's MFMAs
+// start as soon as its slabs are in.
+template <int NR, int CT, class Act, int WV>
+__global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_counted_kernel(
+    const ProjOne P, const uint16_t* __restrict__ X, int K, int M) {
+  extern __shared__ u32x4_t xs[];
+  constexpr int HG = 4;
+  constexpr int kLoads = 2 + 2 * HG;    // memory operations per piece
+  constexpr int kStores = 2 * CT * NR;  // memory operations per finished pair
+  static_assert(NR == 4 && CT == 2, "two full column tiles");
+  constexpr int G = 8;  // K = 1024
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int i = lane & 15, a = lane >> 4;
+  const int ntiles = P.ntiles;
+  const int npairs = ntiles >> 1;
+  const size_t row_bytes = static_cast<size_t>(P.n[0]) * 2;
+  const int stride = static_cast<int>(gridDim.x) * WV;
+  int p = static_cast<int>(blockIdx.x) * WV + wave;
+  const bool active = p < npairs;
+  using L = Layout<Act, true>;
+
+  struct Piece {
+    u32x4_t w[2][HG];
+    uint2 s[2];
+  };
+  // piece h of the tiles at ad[]; the sink's weights when !real
+  auto load = [&](Piece& b, const TileAddr (&ad)[2], int h, bool real) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) b.s[k] = *reinterpret_cast<const uint2*>(ad[k].s + 2 * HG * h);
+#pragma unroll
+    for (int gg = 0; gg < HG; ++gg)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const uint8_t* wp = real ? ad[k].w + static_cast<size_t>(h * HG + gg) * 1024
+                                 : g_piece_sink + lane * 16 + gg * 1024;
+        b.w[k][gg] = load_weights(wp);
+      }
+  };
+  auto pair_addr = [&](TileAddr (&ad)[2], int q) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) ad[k] = tile_addr<true>(P, K, G, 2 * q + k, lane);
+  };
+
+  StageBatch sb0;
+  stage_load(sb0, X, K, 0, M, 0, K, 0);
+  Piece bufA, bufB;
+  TileAddr acur[2];
+  pair_addr(acur, min(p, npairs - 1));
+  load(bufA, acur, 0, true);
+  const u32x4_t* xrow[CT];
+  const float* corr = stream_prologue<CT, Act, false>(xs, xrow, X, K, M, wave, i, a, sb0);
+  if (!active) return;
+
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t part[2][CT];
+  // the finished pair's outputs, two bf16 per register (rows r and r + 1)
+  uint32_t done[2][CT][NR / 2] = {};
+  int done_p = -1;
+  auto store_done = [&]() {
+    // lane's output (row 4a + 16 ct + r, column 32 done_p + 16 k + i); with
+    // no finished pair yet, the same 16 stores go to the sink
+    const bool real = done_p >= 0;
+    uint8_t* base = real ? reinterpret_cast<uint8_t*>(P.y[0]) + static_cast<size_t>(4 * a) * row_bytes +
+                               static_cast<size_t>(32 * done_p + i) * 2
+                         : reinterpret_cast<uint8_t*>(g_store_sink);
+    const size_t rb = real ? row_bytes : 0;
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+          *reinterpret_cast<uint16_t*>(base + static_cast<size_t>(ct * 16 + r) * rb + 32 * k) =
+              static_cast<uint16_t>(done[k][ct][r >> 1] >> (16 * (r & 1)));
+  };
+  // the groups of one piece; kAfter: operations issued after the piece's
+  // last group slabs
+  auto compute = [&](const Piece& cur, int h, auto kAfter) {
+#pragma unroll
+    for (int gg = 0; gg < HG; ++gg) {
+      // cur's scales and group gg of both tiles are in (the scheduler may
+      // not hoist the group's decode above the wait, nor the previous
+      // group's work below it)
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vm_after(decltype(kAfter)::value + 2 * (HG - 1 - gg));
+      __builtin_amdgcn_sched_barrier(0);
+      const int g = h * HG + gg;
+      u32x4_t xa[CT][4];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) load_group_x(xa[ct], xrow[ct] + g * 16, a);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        f32x4_t t[CT];
+        group_tmp_x<NR, CT, L, false>(t, xa, cur.w[k][gg], corr + g * 16 * CT, a);
+        const uint32_t sw = gg < 2 ? cur.s[k].x : cur.s[k].y;
+        const float sc = half_bits_to_f32((sw >> (16 * (gg & 1))) & 0xFFFFu);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int r = 0; r < NR; ++r) part[k][ct][r] = __builtin_fmaf(sc, t[ct][r], part[k][ct][r]);
+      }
+    }
+  };
+  while (true) {
+    // step 0: stores, piece 1's loads, piece 0
+    store_done();
+    load(bufB, acur, 1, true);
+    __builtin_amdgcn_sched_barrier(0);  // stores and loads go out before piece 0's work
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) part[k][ct] = zero;
+    compute(bufA, 0, std::integral_constant<int, kStores + kLoads>{});
+    // step 1: the next pair's piece 0, piece 1
+    const int np = p + stride;
+    const bool has_next = np < npairs;
+    TileAddr anx[2] = {acur[0], acur[1]};
+    if (has_next) pair_addr(anx, np);
+    load(bufA, anx, 0, has_next);
+    __builtin_amdgcn_sched_barrier(0);  // the loads go out before piece 1's work
+    compute(bufB, 1, std::integral_constant<int, kLoads>{});
+    // the tile's one unit ends here: total = 0 + part
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const f32x4_t total = zero + part[k][ct];
+#pragma unroll
+        for (int r = 0; r < NR; r += 2)
+          done[k][ct][r >> 1] = Act::round(Act::kUnit * total[r]) |
+                                (Act::round(Act::kUnit * total[r + 1]) << 16);
+      }
+    done_p = p;
+    if (!has_next) break;
+    acur[0] = anx[0];
+    acur[1] = anx[1];
+    p = np;
+  }
+  store_done();
+}
+
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, class PT = ProjTable>
 __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
     const PT P, const uint16_t* __restrict__ X, int K, int M) {
@@ -1772,6 +1951,11 @@ int proj_one_enabled() {
 // Workgroups per CU of the 8-wave stream kernel (two column tiles).
 // Waves per workgroup of the pair stream kernel (0 = off), and resident
 // workgroups per CU (measurement overrides).
+int stream_pair_counted() {
+  static const int v = env_setting("CUDALM_W4A16_STREAM_PAIR_COUNTED", 1, 0, 1);
+  return v;
+}
+
 int stream_pair_waves() {
   static const int v = env_setting("CUDALM_W4A16_STREAM_PAIR", 8, 0, 8);
   return v == 4 || v == 8 ? v : 0;
@@ -1848,6 +2032,10 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
                            K, M);
         return launch_status();
       };
+      if constexpr (PACKED && NR == 4) {
+        if (G == 8 && M == 32 && P.n[0] % 32 == 0 && stream_pair_counted())
+          return launch_pair(w4a16_stream_pair_counted_kernel<NR, CT, Act, 8>, 8);
+      }
       if (wv == 4)
         return G % 4 == 0 ? launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, true, 4, ProjOne>, 4)
                           : launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, false, 4, ProjOne>, 4);
