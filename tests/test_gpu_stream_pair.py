@@ -76,3 +76,24 @@ def test_counted_and_general_pair_kernels(w4, orc, dev, tmp_path):
             assert ok, (N, M, st)
             print(f"  pair kernels N={N} M={M}: equal, max {st['max_ulp']:.3f} ulp", flush=True)
         del w, s, x, p, y, yt
+
+
+def test_counted_pair_kernel_f16(w4, orc, dev):
+    """The fp16-activation twin through the counted kernel (prepacked, K = 1024,
+    M = 32, N % 32 == 0) equals the file-layout launch (the general pair
+    kernel) bit for bit and is within the fp16 oracle bound."""
+    N, K, M = 4096, 1024, 32
+    W, S = orc.synth_w4a16(0x5F16, N, K)
+    rng = np.random.default_rng(0x5F16)
+    X = rng.normal(0, 1, (M, K)).astype(np.float16).view(np.uint16)
+    w = torch.from_numpy(W).to(dev)
+    s = torch.from_numpy(S.view(np.int16)).to(dev).view(torch.float16)
+    x = torch.from_numpy(X.view(np.int16)).to(dev).view(torch.float16)
+    y_file = w4.gemv_f16(w, s, x, N, K, M)
+    y_packed = w4.gemv_f16_prepacked(w4.repack(w, s, N, K), x, N, K, M)
+    torch.cuda.synchronize()
+    Yf = y_file.view(torch.int16).cpu().numpy().view(np.uint16).reshape(M, N)
+    Yp = y_packed.view(torch.int16).cpu().numpy().view(np.uint16).reshape(M, N)
+    assert np.array_equal(Yp, Yf)
+    ok, st = orc.check_f16_tolerance(Yp, W, S, X, N, K, M)
+    assert ok, st
