@@ -837,196 +837,6 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_kernel(
   }
 }
 
-// Write-only target of the counted pair kernel's first stores (no pair is
-// finished yet, but the step issues its 16 stores so that the number of
-// memory operations per step is fixed). Nothing reads it.
-__device__ __align__(256) uint16_t g_store_sink[64];
-
-// s_waitcnt vmcnt(v), expcnt and lgkmcnt at their maxima, for the counts
-// the counted kernel uses with TPW = 2 (v is a constant once the caller is
-// unrolled; any other count waits for everything).
-constexpr int vm_wait(int v) { return (v & 15) | ((v >> 4) << 14) | 0x0F70; }
-__device__ __forceinline__ void wait_vm_after(int v) {
-  switch (v) {
-#define CUDALM_VM_CASE(n) \
-  case n:                 \
-    __builtin_amdgcn_s_waitcnt(vm_wait(n)); \
-    break;
-    CUDALM_VM_CASE(10) CUDALM_VM_CASE(12) CUDALM_VM_CASE(14) CUDALM_VM_CASE(16)
-    CUDALM_VM_CASE(26) CUDALM_VM_CASE(28) CUDALM_VM_CASE(30) CUDALM_VM_CASE(32)
-#undef CUDALM_VM_CASE
-    default:
-      __builtin_amdgcn_s_waitcnt(vm_wait(0));
-  }
-}
-
-// Counted stream kernel: the stream kernels' work and per-output operation
-// sequence for one prepacked projection with K = 1024 (a tile is two pieces
-// of 4 groups) and N % 16 == 0, each wave streaming TPW adjacent tiles at a
-// time (TPW = 2: the pair kernel's M = 32 plan, which also needs
-// N % 32 == 0; TPW = 1 for M <= 16 measured even with the piece stream
-// kernel on the LM head, 21.4-21.7 against 21.2-21.5 us at M = 1, and is
-// not launched), with the waits for its loads placed by the kernel. Loads and stores share one in-order memory counter, and the
-// compiler's own waits, which must hold on every path through the loop,
-// also wait for stores issued after the loads they need. Here the loop body
-// is one tile group in two steps with fixed memory operations:
-//   step 0: the previous group's TPW * CT * NR output stores (rows past M,
-//           and the first pass's stores, go to a sink), the loads of piece
-//           1 (the tiles' scales, then their group slabs group by group),
-//           then piece 0's groups;
-//   step 1: the loads of the next group's piece 0 (the sink's weights past
-//           the last one), then piece 1's groups.
-// Each group waits for the operations issued before its slabs, so the
-// stores overlap a step of loads and compute and a group's MFMAs start as
-// soon as its slabs are in; the scheduler may not move work across those
-// waits. The compiler still adds any wait its own analysis needs, so the
-// explicit ones cannot under-wait.
-template <int TPW, int NR, int CT, class Act, int WV>
-__global__ __launch_bounds__(WV * 64) void w4a16_stream_counted_kernel(
-    const ProjOne P, const uint16_t* __restrict__ X, int K, int M) {
-  extern __shared__ u32x4_t xs[];
-  constexpr int HG = 4;
-  constexpr int kLoads = TPW * (1 + HG);    // memory operations per piece
-  constexpr int kStores = TPW * CT * NR;    // memory operations per finished group
-  constexpr int G = 8;                      // K = 1024
-  const int lane = threadIdx.x & 63;
-  const int wave = wave_id();
-  const int i = lane & 15, a = lane >> 4;
-  const int ntiles = P.ntiles;
-  const int ngroups = ntiles / TPW;
-  const size_t row_bytes = static_cast<size_t>(P.n[0]) * 2;
-  const int stride = static_cast<int>(gridDim.x) * WV;
-  int p = static_cast<int>(blockIdx.x) * WV + wave;
-  const bool active = p < ngroups;
-  using L = Layout<Act, true>;
-
-  struct Piece {
-    u32x4_t w[TPW][HG];
-    uint2 s[TPW];
-  };
-  // piece h of the tiles at ad[]; the sink's weights when !real
-  auto load = [&](Piece& b, const TileAddr (&ad)[TPW], int h, bool real) {
-#pragma unroll
-    for (int k = 0; k < TPW; ++k) b.s[k] = *reinterpret_cast<const uint2*>(ad[k].s + 2 * HG * h);
-#pragma unroll
-    for (int gg = 0; gg < HG; ++gg)
-#pragma unroll
-      for (int k = 0; k < TPW; ++k) {
-        const uint8_t* wp = real ? ad[k].w + static_cast<size_t>(h * HG + gg) * 1024
-                                 : g_piece_sink + lane * 16 + gg * 1024;
-        b.w[k][gg] = load_weights(wp);
-      }
-  };
-  auto group_addr = [&](TileAddr (&ad)[TPW], int q) {
-#pragma unroll
-    for (int k = 0; k < TPW; ++k) ad[k] = tile_addr<true>(P, K, G, TPW * q + k, lane);
-  };
-
-  StageBatch sb0;
-  stage_load(sb0, X, K, 0, M, 0, K, 0);
-  Piece bufA, bufB;
-  TileAddr acur[TPW];
-  group_addr(acur, min(p, ngroups - 1));
-  load(bufA, acur, 0, true);
-  const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT, Act, false>(xs, xrow, X, K, M, wave, i, a, sb0);
-  if (!active) return;
-
-  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f32x4_t part[TPW][CT];
-  // the finished group's outputs, two bf16 per register (rows r and r + 1;
-  // NR == 1: one)
-  constexpr int NW = (NR + 1) / 2;
-  uint32_t done[TPW][CT][NW] = {};
-  int done_p = -1;
-  auto store_done = [&]() {
-    // lane's output (row 4a + 16 ct + r, column 16 (TPW done_p + k) + i);
-    // with no finished group yet, the same stores go to the sink
-    const bool real = done_p >= 0;
-    uint8_t* base = real ? reinterpret_cast<uint8_t*>(P.y[0]) + static_cast<size_t>(4 * a) * row_bytes +
-                               static_cast<size_t>(16 * TPW * done_p + i) * 2
-                         : reinterpret_cast<uint8_t*>(g_store_sink);
-    const size_t rb = real ? row_bytes : 0;
-#pragma unroll
-    for (int k = 0; k < TPW; ++k)
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          // rows past M: this lane's store goes to the sink (the same count of stores)
-          uint8_t* dst = ct * 16 + 4 * a + r < M ? base + static_cast<size_t>(ct * 16 + r) * rb + 32 * k
-                                                 : reinterpret_cast<uint8_t*>(g_store_sink);
-          *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(done[k][ct][r >> 1] >> (16 * (r & 1)));
-        }
-  };
-  // the groups of one piece; kAfter: operations issued after the piece's
-  // last group slabs
-  auto compute = [&](const Piece& cur, int h, auto kAfter) {
-#pragma unroll
-    for (int gg = 0; gg < HG; ++gg) {
-      // cur's scales and group gg of its tiles are in (the scheduler may not
-      // hoist the group's decode above the wait, nor the previous group's
-      // work below it)
-      __builtin_amdgcn_sched_barrier(0);
-      wait_vm_after(decltype(kAfter)::value + TPW * (HG - 1 - gg));
-      __builtin_amdgcn_sched_barrier(0);
-      const int g = h * HG + gg;
-      u32x4_t xa[CT][4];
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) load_group_x(xa[ct], xrow[ct] + g * 16, a);
-#pragma unroll
-      for (int k = 0; k < TPW; ++k) {
-        f32x4_t t[CT];
-        group_tmp_x<NR, CT, L, false>(t, xa, cur.w[k][gg], corr + g * 16 * CT, a);
-        const uint32_t sw = gg < 2 ? cur.s[k].x : cur.s[k].y;
-        const float sc = half_bits_to_f32((sw >> (16 * (gg & 1))) & 0xFFFFu);
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-          for (int r = 0; r < NR; ++r) part[k][ct][r] = __builtin_fmaf(sc, t[ct][r], part[k][ct][r]);
-      }
-    }
-  };
-  while (true) {
-    // step 0: stores, piece 1's loads, piece 0
-    store_done();
-    load(bufB, acur, 1, true);
-    __builtin_amdgcn_sched_barrier(0);  // stores and loads go out before piece 0's work
-#pragma unroll
-    for (int k = 0; k < TPW; ++k)
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) part[k][ct] = zero;
-    compute(bufA, 0, std::integral_constant<int, kStores + kLoads>{});
-    // step 1: the next group's piece 0, piece 1
-    const int np = p + stride;
-    const bool has_next = np < ngroups;
-    TileAddr anx[TPW];
-#pragma unroll
-    for (int k = 0; k < TPW; ++k) anx[k] = acur[k];
-    if (has_next) group_addr(anx, np);
-    load(bufA, anx, 0, has_next);
-    __builtin_amdgcn_sched_barrier(0);  // the loads go out before piece 1's work
-    compute(bufB, 1, std::integral_constant<int, kLoads>{});
-    // the tile's one unit ends here: total = 0 + part
-#pragma unroll
-    for (int k = 0; k < TPW; ++k)
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const f32x4_t total = zero + part[k][ct];
-#pragma unroll
-        for (int r = 0; r < NR; r += 2)
-          done[k][ct][r >> 1] = Act::round(Act::kUnit * total[r]) |
-                                (r + 1 < NR ? Act::round(Act::kUnit * total[r + 1]) << 16 : 0u);
-      }
-    done_p = p;
-    if (!has_next) break;
-#pragma unroll
-    for (int k = 0; k < TPW; ++k) acur[k] = anx[k];
-    p = np;
-  }
-  store_done();
-}
-
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, class PT = ProjTable>
 __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
     const PT P, const uint16_t* __restrict__ X, int K, int M) {
@@ -1962,11 +1772,6 @@ int proj_one_enabled() {
 // Workgroups per CU of the 8-wave stream kernel (two column tiles).
 // Waves per workgroup of the pair stream kernel (0 = off), and resident
 // workgroups per CU (measurement overrides).
-int stream_pair_counted() {
-  static const int v = env_setting("CUDALM_W4A16_STREAM_PAIR_COUNTED", 1, 0, 1);
-  return v;
-}
-
 int stream_pair_waves() {
   static const int v = env_setting("CUDALM_W4A16_STREAM_PAIR", 8, 0, 8);
   return v == 4 || v == 8 ? v : 0;
@@ -2043,10 +1848,6 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
                            K, M);
         return launch_status();
       };
-      if constexpr (PACKED && NR == 4) {
-        if (G == 8 && M == 32 && P.n[0] % 32 == 0 && stream_pair_counted())
-          return launch_pair(w4a16_stream_counted_kernel<2, NR, CT, Act, 8>, 8);
-      }
       if (wv == 4)
         return G % 4 == 0 ? launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, true, 4, ProjOne>, 4)
                           : launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, false, 4, ProjOne>, 4);
