@@ -591,6 +591,8 @@ __device__ __forceinline__ TileAddr tile_addr(const PT& P, int K, int G, int t, 
 template <int HG, bool PACKED, bool SVEC, bool FULL>
 __device__ __forceinline__ void stream_load_piece(StreamPiece<HG>& h, TileAddr ad, int G, int g0) {
   static_assert(HG == 1 || HG == 2 || HG == 4, "piece of 1, 2 or 4 groups");
+  // a piece past a wave's last one is read from g_piece_sink: it must fit
+  static_assert(HG * 1024 + 64 * 16 <= sizeof(g_piece_sink), "the sink must hold a whole piece");
   constexpr int kStep = PACKED ? 1024 : 64;  // bytes between groups of one lane
   const uint8_t* wp = ad.w + static_cast<size_t>(g0) * kStep;
 #pragma unroll
