@@ -212,7 +212,9 @@ def graph_time(torch, fn, reps: int, stream):
 
 def bench_bf16_lm_head(torch, lib, dev, stream, sraw, reps: int = 40):
     """Tied bf16 LM head (bf16_gemv / batch_bf16_gemv), M = 1 and 8, four
-    rotating 508 MB weight copies; per-launch event timing."""
+    rotating 508 MB weight copies; per-launch event timing. The `_prepacked`
+    lines read a tile-major copy made at load time (cudalm_bf16_repack,
+    outside the timed region) through cudalm_bf16_gemv_prepacked."""
     Nb, Kb = LM_HEAD
     embs = []
     for c in range(4):
@@ -231,7 +233,25 @@ def bench_bf16_lm_head(torch, lib, dev, stream, sraw, reps: int = 40):
         bf[f"M{Mb}"] = {"kernel_us": round(per * 1e6, 2), "GBps": round(byts / per / 1e9, 1),
                         "frac_hbm_peak": round(byts / per / 1e9 / HBM_PEAK_GBS, 4),
                         "algorithmic_bytes": byts}
+    packs = []
+    for e in embs:
+        pk = torch.empty(Nb * Kb, dtype=torch.bfloat16, device=dev)
+        assert lib.cudalm_bf16_repack(e.data_ptr(), pk.data_ptr(), Nb, Kb, sraw) == 0
+        packs.append(pk)
+    torch.cuda.synchronize()
     del embs
+    for Mb in (1, 8):
+        xb = synth_act(torch, Mb, Kb, 0xB16 + Mb, dev)
+        yb = torch.empty((Mb, Nb), dtype=torch.bfloat16, device=dev)
+        xbp, ybp = xb.data_ptr(), yb.data_ptr()
+        L = [(lambda pp=p.data_ptr(): lib.cudalm_bf16_gemv_prepacked(pp, xbp, ybp, Nb, Kb, Mb, sraw))
+             for p in packs]
+        per = stream_time(torch, L, reps, 8, stream)
+        byts = 2 * Nb * Kb + 2 * Mb * Kb + 2 * Mb * Nb
+        bf[f"M{Mb}_prepacked"] = {"kernel_us": round(per * 1e6, 2), "GBps": round(byts / per / 1e9, 1),
+                                  "frac_hbm_peak": round(byts / per / 1e9 / HBM_PEAK_GBS, 4),
+                                  "algorithmic_bytes": byts}
+    del packs
     return bf
 
 

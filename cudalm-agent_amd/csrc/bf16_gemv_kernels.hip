@@ -53,6 +53,24 @@ __device__ __forceinline__ void bf16_unit_load(Bf16Unit& v, const uint16_t* __re
     v.w[j] = *reinterpret_cast<const u32x4_t*>(wrow + min(u * kUnitK + 32 * j + 8 * a, K - 8));
 }
 
+// Tile-major layout (cudalm_bf16_repack): the unit u of tile t is 8
+// consecutive 1 KB slabs, slab j holding, at byte 16 l, lane l's 16 bytes of
+// MFMA step j (row 16 t + l % 16, k = 256 u + 32 j + 8 (l / 16)), so every
+// wave-wide load reads 1 KB contiguous. Requires N % 16 == 0, K % 256 == 0.
+// Read-only target of a wave's last, unused unit load on the packed copy:
+// one unit (8 slabs of 1 KB), never written. The loop's loads stay
+// unconditional without re-reading a non-temporally loaded unit from HBM.
+__device__ __align__(256) uint16_t g_bf16_unit_sink[kSteps * 512];
+
+__device__ __forceinline__ void bf16_unit_load_packed(Bf16Unit& v, const uint16_t* __restrict__ Wp,
+                                                      int U, int tile, int u, int lane, bool real) {
+  const uint16_t* slab =
+      (real ? Wp + (static_cast<size_t>(tile) * U + u) * (kSteps * 512) : g_bf16_unit_sink) + lane * 8;
+#pragma unroll
+  for (int j = 0; j < kSteps; ++j)
+    v.w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(slab + j * 512));
+}
+
 template <int CT>
 __device__ __forceinline__ void bf16_unit_mma(f32x4_t (&acc)[CT], const Bf16Unit& v,
                                               const u32x4_t* const (&xrow)[CT], int u, int K,
@@ -71,7 +89,7 @@ __device__ __forceinline__ void bf16_unit_mma(f32x4_t (&acc)[CT], const Bf16Unit
 // LDS = mc * (32 * ceil(K/256) + 1) * 16 bytes; chunk y covers activation
 // rows [y * mc, y * mc + mc) and mc <= 16 * CT. Requires K % 8 == 0 and
 // 16 B aligned W and X bases.
-template <int CT>
+template <int CT, bool PACKED = false>
 __global__ __launch_bounds__(kWaves * 64) void bf16_gemv_stream_kernel(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
     int N, int K, int M, int mc) {
@@ -89,7 +107,10 @@ __global__ __launch_bounds__(kWaves * 64) void bf16_gemv_stream_kernel(
 
   // first unit's weights fly while the activations are staged
   Bf16Unit cur, nxt;
-  bf16_unit_load(cur, W, N, K, min(t, ntiles - 1), 0, lane);
+  if constexpr (PACKED)
+    bf16_unit_load_packed(cur, W, U, min(t, ntiles - 1), 0, lane, true);
+  else
+    bf16_unit_load(cur, W, N, K, min(t, ntiles - 1), 0, lane);
   const int nb = U * (kUnitK / 8);
   for (int e = threadIdx.x; e < mrows * nb; e += blockDim.x) {
     const int mm = e / nb;
@@ -120,7 +141,10 @@ __global__ __launch_bounds__(kWaves * 64) void bf16_gemv_stream_kernel(
     const bool has_next = nt < ntiles;
     // past the last unit, re-read the current one (cache hits) instead of
     // branching around the loads
-    bf16_unit_load(nxt, W, N, K, has_next ? nt : t, has_next ? nu : u, lane);
+    if constexpr (PACKED)
+      bf16_unit_load_packed(nxt, W, U, nt, nu, lane, has_next);
+    else
+      bf16_unit_load(nxt, W, N, K, has_next ? nt : t, has_next ? nu : u, lane);
     bf16_unit_mma<CT>(acc, cur, xrow, u, K, a);
     if (u == U - 1) {
       const int n = t * kTile + i;
@@ -184,11 +208,11 @@ int stream_wgs_per_cu() {
   return occ;
 }
 
-template <int CT>
+template <int CT, bool PACKED = false>
 int launch_stream_ct(const uint16_t* W, const uint16_t* X, uint16_t* Y, int N, int K, int M,
                      int mc, hipStream_t stream) {
   const size_t lds = stream_lds(K, mc);
-  auto kern = bf16_gemv_stream_kernel<CT>;
+  auto kern = bf16_gemv_stream_kernel<CT, PACKED>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
   const int ntiles = (N + kTile - 1) / kTile;
   const int per_cu = static_cast<int>(kLdsMax / lds) < stream_wgs_per_cu()
@@ -205,12 +229,32 @@ int launch_stream_ct(const uint16_t* W, const uint16_t* X, uint16_t* Y, int N, i
   return launch_status();
 }
 
+template <bool PACKED = false>
 int launch_stream(const uint16_t* W, const uint16_t* X, uint16_t* Y, int N, int K, int M,
                   hipStream_t stream) {
   const int mc = stream_rows_per_chunk(K, M);
   if (mc < 1) return CUDALM_W4A16_EVARIANT;
-  if (mc > 16) return launch_stream_ct<2>(W, X, Y, N, K, M, mc, stream);
-  return launch_stream_ct<1>(W, X, Y, N, K, M, mc, stream);
+  if (mc > 16) return launch_stream_ct<2, PACKED>(W, X, Y, N, K, M, mc, stream);
+  return launch_stream_ct<1, PACKED>(W, X, Y, N, K, M, mc, stream);
+}
+
+// One thread per 16-byte chunk of the tile-major layout.
+__global__ __launch_bounds__(256) void bf16_repack_kernel(const uint16_t* __restrict__ W,
+                                                          uint16_t* __restrict__ Wp, int K,
+                                                          long long nchunks) {
+  const long long c = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= nchunks) return;
+  const int U = K / kUnitK;
+  const int lane = static_cast<int>(c & 63);
+  const long long slab = c >> 6;  // (tile * U + u) * kSteps + j
+  const int j = static_cast<int>(slab % kSteps);
+  const long long tu = slab / kSteps;
+  const int u = static_cast<int>(tu % U);
+  const long long tile = tu / U;
+  const long long row = tile * kTile + (lane & 15);
+  const int k = u * kUnitK + 32 * j + 8 * (lane >> 4);
+  *reinterpret_cast<u32x4_t*>(Wp + c * 8) =
+      *reinterpret_cast<const u32x4_t*>(W + row * K + k);
 }
 
 int launch_scalar(const uint16_t* W, const uint16_t* X, uint16_t* Y, int N, int K, int M,
@@ -260,6 +304,31 @@ int cudalm_bf16_gemv_variant(const uint16_t* weight, const uint16_t* x, uint16_t
 int cudalm_bf16_gemv(const uint16_t* weight, const uint16_t* x, uint16_t* y, int N, int K, int M,
                      hipStream_t stream) {
   return cudalm_bf16_gemv_variant(weight, x, y, N, K, M, CUDALM_BF16_VARIANT_AUTO, stream);
+}
+
+size_t cudalm_bf16_packed_bytes(int N, int K) {
+  return static_cast<size_t>(N) * static_cast<size_t>(K) * 2;
+}
+
+int cudalm_bf16_repack(const uint16_t* weight, void* packed, int N, int K, hipStream_t stream) {
+  if (int rc = check_shape(N, K, 1)) return rc;
+  if (!weight || !packed) return CUDALM_W4A16_ENULL;
+  if (N % kTile != 0 || K % kUnitK != 0) return CUDALM_W4A16_EINVAL;
+  if (!aligned(weight, 16) || !aligned(packed, 16)) return CUDALM_W4A16_EALIGN;
+  const long long nchunks = static_cast<long long>(N) * K / 8;
+  hipLaunchKernelGGL(bf16_repack_kernel, dim3(static_cast<unsigned>((nchunks + 255) / 256)),
+                     dim3(256), 0, stream, weight, static_cast<uint16_t*>(packed), K, nchunks);
+  return launch_status();
+}
+
+int cudalm_bf16_gemv_prepacked(const void* packed, const uint16_t* x, uint16_t* y, int N, int K,
+                               int M, hipStream_t stream) {
+  if (int rc = check_shape(N, K, M)) return rc;
+  if (!packed || !x || !y) return CUDALM_W4A16_ENULL;
+  if (N % kTile != 0 || K % kUnitK != 0) return CUDALM_W4A16_EINVAL;
+  if (!aligned(packed, 16) || !aligned(x, 16) || !aligned(y, 2)) return CUDALM_W4A16_EALIGN;
+  if (stream_rows_per_chunk(K, M) < 1) return CUDALM_W4A16_EVARIANT;
+  return launch_stream<true>(static_cast<const uint16_t*>(packed), x, y, N, K, M, stream);
 }
 
 int cudalm_bf16_gemv_kernel_regs(int variant) {

@@ -66,6 +66,9 @@ _SIGS = {
     "cudalm_v2_upload": ([_P, ctypes.c_char_p, _P, _SZ, _P], _I),
     "cudalm_bf16_gemv_variant": ([_P, _P, _P, _I, _I, _I, _I, _P], _I),
     "cudalm_bf16_gemv_kernel_regs": ([_I], _I),
+    "cudalm_bf16_packed_bytes": ([_I, _I], _SZ),
+    "cudalm_bf16_repack": ([_P, _P, _I, _I, _P], _I),
+    "cudalm_bf16_gemv_prepacked": ([_P, _P, _P, _I, _I, _I, _P], _I),
 }
 for _name, (_args, _ret) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -363,6 +366,25 @@ def bf16_gemv_any(weight, x, N: int, K: int, M: int = 1, y=None,
     rc = _lib.cudalm_bf16_gemv_variant(_ptr(weight), _ptr(x), _ptr(y), N, K, M, variant,
                                        _stream(stream))
     _check(rc, "cudalm_bf16_gemv")
+    return y
+
+
+def bf16_repack(weight, N: int, K: int, out=None, stream=None):
+    """Tile-major copy of a bf16 [N, K] weight for bf16_gemv_prepacked."""
+    import torch
+
+    if out is None:
+        out = torch.empty(N * K, dtype=torch.bfloat16, device=weight.device)
+    rc = _lib.cudalm_bf16_repack(_ptr(weight), _ptr(out), N, K, _stream(stream))
+    _check(rc, "cudalm_bf16_repack")
+    return out
+
+
+def bf16_gemv_prepacked(packed, x, N: int, K: int, M: int = 1, y=None, stream=None):
+    """bf16_gemv_any on a bf16_repack copy (same bits)."""
+    y = _out(y, M, N, x)
+    rc = _lib.cudalm_bf16_gemv_prepacked(_ptr(packed), _ptr(x), _ptr(y), N, K, M, _stream(stream))
+    _check(rc, "cudalm_bf16_gemv_prepacked")
     return y
 
 

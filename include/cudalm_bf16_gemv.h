@@ -26,6 +26,7 @@
 #ifndef CUDALM_BF16_GEMV_H
 #define CUDALM_BF16_GEMV_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #include <hip/hip_runtime_api.h>
@@ -54,6 +55,27 @@ int cudalm_bf16_gemv_variant(const uint16_t* weight, const uint16_t* x,
 
 /* Registers (VGPR + AGPR) of a variant's kernel; -1 if unavailable. */
 int cudalm_bf16_gemv_kernel_regs(int variant);
+
+/* Load-time tile repack of a bf16 weight (no counterpart in the reference;
+ * it hooks where the tied embedding is uploaded, the upload lambda of
+ * src/runtime/weight_loader_v2.cpp:435-441, like cudalm_w4a16_repack).
+ * The packed copy is tile-major: for each 16-row tile and each 256-k unit,
+ * eight 1 KB slabs, slab j holding at byte 16 l the 16 bytes MFMA lane l
+ * reads at step j (row 16 t + l % 16, k = 256 u + 32 j + 8 (l / 16)), so
+ * every wave-wide load of the GEMV reads 1 KB contiguous. The row-major
+ * original stays valid (the embedding lookup reads it); the copy is a
+ * second N*K*2 bytes. Requires N % 16 == 0, K % 256 == 0 and 16-byte
+ * aligned bases (CUDALM_W4A16_EINVAL / EALIGN otherwise). */
+size_t cudalm_bf16_packed_bytes(int N, int K);
+int cudalm_bf16_repack(const uint16_t* weight, void* packed, int N, int K,
+                       hipStream_t stream);
+
+/* cudalm_bf16_gemv on the packed copy: the same kernel and the same result
+ * bits, reading 1 KB contiguous per wave load. N % 16 == 0, K % 256 == 0,
+ * 16-byte aligned packed and x bases, and x rows that fit the LDS
+ * (CUDALM_W4A16_EVARIANT otherwise). */
+int cudalm_bf16_gemv_prepacked(const void* packed, const uint16_t* x, uint16_t* y,
+                               int N, int K, int M, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -76,6 +76,22 @@ def test_bf16_gemv_preconditions_rejected_before_device(w4):
     assert p(fake, fake, fake, 1 << 30, 16, 1) == w4.ERANGE
 
 
+def test_bf16_repack_preconditions_rejected_before_device(w4):
+    # include/cudalm_bf16_gemv.h: the packed path needs N % 16 == 0,
+    # K % 256 == 0 and 16-byte aligned bases
+    fake = 0x1000
+    lib = w4.lib()
+    assert lib.cudalm_bf16_packed_bytes(32, 512) == 32 * 512 * 2
+    assert lib.cudalm_bf16_repack(fake, fake, 17, 256, None) == w4.EINVAL
+    assert lib.cudalm_bf16_repack(fake, fake, 16, 128, None) == w4.EINVAL
+    assert lib.cudalm_bf16_repack(None, fake, 16, 256, None) == w4.ENULL
+    assert lib.cudalm_bf16_repack(fake + 2, fake, 16, 256, None) == w4.EALIGN
+    assert lib.cudalm_bf16_gemv_prepacked(fake, fake, fake, 16, 200, 1, None) == w4.EINVAL
+    assert lib.cudalm_bf16_gemv_prepacked(fake, fake, None, 16, 256, 1, None) == w4.ENULL
+    assert lib.cudalm_bf16_gemv_prepacked(fake, fake + 2, fake, 16, 256, 1, None) == w4.EALIGN
+    assert lib.cudalm_bf16_gemv_prepacked(fake, fake, fake, 16, 256, 0, None) == w4.EINVAL
+
+
 def test_packed_bytes(w4):
     assert w4.packed_bytes(16, 128) == 1024 + 256
     assert w4.packed_bytes(17, 128) == 2 * (1024 + 256)

@@ -173,3 +173,34 @@ def test_non_default_stream(w4, orc, dev):
         w4.bf16_gemv_any(w, x, N, K, M, y=y, stream=st)
     st.synchronize()
     assert np.array_equal(down(y).reshape(M, N), ref)
+
+
+def test_repack_layout(w4, dev):
+    """The tile-major copy (include/cudalm_bf16_gemv.h): slab j of unit u of
+    tile t holds, at 16-byte block l, row 16 t + l % 16, k = 256 u + 32 j +
+    8 (l / 16) .. + 7; restated here with a numpy reshape."""
+    N, K = 48, 512
+    rng = np.random.default_rng(0xB1)
+    W = rng.integers(0, 1 << 16, size=(N, K), dtype=np.uint16)
+    (w,) = up(dev, W)
+    P = down(w4.bf16_repack(w, N, K))
+    # [t, i, u, j, a, e] -> [t, u, j, a, i, e]
+    exp = W.reshape(N // 16, 16, K // 256, 8, 4, 8).transpose(0, 2, 3, 4, 1, 5).reshape(-1)
+    assert np.array_equal(P, exp)
+
+
+@pytest.mark.parametrize("N,K,M", [(16, 256, 1), (4096, 1024, 1), (4096, 1024, 8),
+                                   (1024, 2048, 17), (4096, 1024, 32), (512, 1024, 40),
+                                   (248320, 1024, 1), (248320, 1024, 8)])
+def test_prepacked_equals_row_major(w4, orc, dev, N, K, M):
+    """The packed copy gives the row-major call's bits (same kernel, same
+    MFMA chain per output) and so the same oracle bound."""
+    W = orc.f32_to_bf16(orc.synth_normal(0xB0 + N + K, 0.02, N * K)).reshape(N, K)
+    X = orc.synth_act(0xB1 + M, M, K)
+    w, x = up(dev, W, X)
+    Y = run(w4, w, x, N, K, M)
+    p = w4.bf16_repack(w, N, K)
+    Yp = down(w4.bf16_gemv_prepacked(p, x, N, K, M)).reshape(M, N)
+    assert np.array_equal(Yp, Y), (N, K, M)
+    if N * K <= 4096 * 2048:
+        check(orc, Yp, W, X, N, K, M, "prepacked", ref_cmp=False)
