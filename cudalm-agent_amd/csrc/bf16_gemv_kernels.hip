@@ -307,6 +307,7 @@ int cudalm_bf16_gemv(const uint16_t* weight, const uint16_t* x, uint16_t* y, int
 }
 
 size_t cudalm_bf16_packed_bytes(int N, int K) {
+  if (N < 1 || K < 1 || N % kTile != 0 || K % kUnitK != 0) return 0;
   return static_cast<size_t>(N) * static_cast<size_t>(K) * 2;
 }
 

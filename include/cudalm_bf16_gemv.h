@@ -65,7 +65,9 @@ int cudalm_bf16_gemv_kernel_regs(int variant);
  * every wave-wide load of the GEMV reads 1 KB contiguous. The row-major
  * original stays valid (the embedding lookup reads it); the copy is a
  * second N*K*2 bytes. Requires N % 16 == 0, K % 256 == 0 and 16-byte
- * aligned bases (CUDALM_W4A16_EINVAL / EALIGN otherwise). */
+ * aligned bases (CUDALM_W4A16_EINVAL / EALIGN otherwise). The packed size
+ * is N * K * 2 bytes; cudalm_bf16_packed_bytes returns 0 for a shape the
+ * packed path does not take. */
 size_t cudalm_bf16_packed_bytes(int N, int K);
 int cudalm_bf16_repack(const uint16_t* weight, void* packed, int N, int K,
                        hipStream_t stream);

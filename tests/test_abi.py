@@ -82,6 +82,9 @@ def test_bf16_repack_preconditions_rejected_before_device(w4):
     fake = 0x1000
     lib = w4.lib()
     assert lib.cudalm_bf16_packed_bytes(32, 512) == 32 * 512 * 2
+    assert lib.cudalm_bf16_packed_bytes(17, 512) == 0
+    assert lib.cudalm_bf16_packed_bytes(32, 100) == 0
+    assert lib.cudalm_bf16_packed_bytes(-16, 256) == 0
     assert lib.cudalm_bf16_repack(fake, fake, 17, 256, None) == w4.EINVAL
     assert lib.cudalm_bf16_repack(fake, fake, 16, 128, None) == w4.EINVAL
     assert lib.cudalm_bf16_repack(None, fake, 16, 256, None) == w4.ENULL
