@@ -16,7 +16,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB = os.path.join(PKG_DIR, "cudalm_w4a16", "libcudalm_w4a16.so")
-SOURCES = ["w4a16_kernels.hip", "w4a16_gemm.hip", "bf16_gemv_kernels.hip", "w4a16_host.hip",
+SOURCES = ["w4a16_kernels.hip", "w4a16_chain.hip", "w4a16_gemm.hip", "bf16_gemv_kernels.hip", "w4a16_host.hip",
            "cudalm_v2_reader.cpp"]
 
 HIPCC_FLAGS = [

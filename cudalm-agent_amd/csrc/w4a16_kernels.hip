@@ -2340,6 +2340,7 @@ const char* cudalm_w4a16_strerror(int code) {
     case -7: return "weight file breaks a .cudalm v2 container rule";
     case -8: return "weight file could not be opened or mapped";
     case -9: return "tensor not found, or not of the expected dtype / shape";
+    case CUDALM_W4A16_ETIMEOUT: return "a chain stage waited past its bound (outputs unspecified)";
     default: return "unknown error code";
   }
 }

@@ -69,6 +69,11 @@ _SIGS = {
     "cudalm_bf16_packed_bytes": ([_I, _I], _SZ),
     "cudalm_bf16_repack": ([_P, _P, _I, _I, _P], _I),
     "cudalm_bf16_gemv_prepacked": ([_P, _P, _P, _I, _I, _I, _P], _I),
+    "cudalm_w4a16_chain_workspace_bytes": ([_I], _SZ),
+    "cudalm_w4a16_chain_plan": ([_P, _I, _I, _I, _P, _SZ, _P, _P], _I),
+    "cudalm_w4a16_chain_run": ([_P, _P], _I),
+    "cudalm_w4a16_chain_status": ([_P, _P], _I),
+    "cudalm_w4a16_gemv_bf16_chain": ([_P, _I, _I, _I, _P, _SZ, _P], _I),
 }
 for _name, (_args, _ret) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -87,6 +92,7 @@ EVARIANT = -6
 V2_EFORMAT = -7
 V2_EIO = -8
 V2_ENOTFOUND = -9
+ETIMEOUT = -10
 
 VARIANT_AUTO = 0
 VARIANT_STREAM = 1
@@ -114,12 +120,25 @@ BF16_VARIANTS = {"auto": BF16_VARIANT_AUTO, "stream": BF16_VARIANT_STREAM,
 
 GROUP = 128
 MAX_PROJ = 8
+MAX_STAGES = 256
 
 
 class Proj(ctypes.Structure):
     """struct cudalm_w4a16_proj (include/cudalm_w4a16.h)."""
     _fields_ = [("weight", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("y", ctypes.c_void_p),
                 ("N", ctypes.c_int)]
+
+
+class Stage(ctypes.Structure):
+    """struct cudalm_w4a16_stage (include/cudalm_w4a16.h)."""
+    _fields_ = [("projs", ctypes.c_void_p), ("count", ctypes.c_int), ("x", ctypes.c_void_p),
+                ("K", ctypes.c_int), ("dep", ctypes.c_int)]
+
+
+class ChainHandle(ctypes.Structure):
+    """struct cudalm_w4a16_chain (include/cudalm_w4a16.h), filled by the plan."""
+    _fields_ = [("workspace", ctypes.c_void_p), ("n_stages", ctypes.c_int), ("M", ctypes.c_int),
+                ("prepacked", ctypes.c_int), ("grid", ctypes.c_int), ("gt_max", ctypes.c_int)]
 
 
 class W4A16Error(RuntimeError):
@@ -292,6 +311,46 @@ def gemv_multi(weights, scales, x, Ns, K: int, M: int = 1, ys=None, prepacked: b
                                            K, M, int(prepacked), _stream(stream))
     _check(rc, "cudalm_w4a16_gemv_bf16_multi")
     return ys
+
+
+class Chain:
+    """A planned stage chain (cudalm_w4a16_chain_plan) and its workspace.
+
+    stages: list of (items, x, K, dep) with items a list of
+    (weight_ptr, scale_ptr_or_None, y_ptr, N) sharing x (a tensor or a raw
+    address); dep is the index of an earlier stage or -1. run() is one kernel
+    launch (capturable); status() synchronizes and raises W4A16Error on a
+    timed-out wait."""
+
+    def __init__(self, stages, M: int, prepacked: bool = True, device=None, stream=None):
+        import torch
+
+        self._arrays = [proj_array(items) for items, _x, _K, _dep in stages]
+        st = (Stage * len(stages))()
+        for k, ((items, x, K, dep), arr) in enumerate(zip(stages, self._arrays)):
+            st[k].projs = ctypes.cast(arr, ctypes.c_void_p)
+            st[k].count = len(items)
+            st[k].x = x if isinstance(x, int) else _ptr(x)
+            st[k].K = K
+            st[k].dep = dep
+        self._stages = st
+        nbytes = _lib.cudalm_w4a16_chain_workspace_bytes(len(stages))
+        if nbytes == 0:
+            raise ValueError(f"chain of {len(stages)} stages: at most {MAX_STAGES}")
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=device or "cuda")
+        self.handle = ChainHandle()
+        rc = _lib.cudalm_w4a16_chain_plan(ctypes.cast(st, ctypes.c_void_p), len(stages), M,
+                                          int(prepacked), self.workspace.data_ptr(), nbytes,
+                                          ctypes.byref(self.handle), _stream(stream))
+        _check(rc, "cudalm_w4a16_chain_plan")
+
+    def run(self, stream=None) -> None:
+        _check(_lib.cudalm_w4a16_chain_run(ctypes.byref(self.handle), _stream(stream)),
+               "cudalm_w4a16_chain_run")
+
+    def status(self, stream=None) -> None:
+        _check(_lib.cudalm_w4a16_chain_status(ctypes.byref(self.handle), _stream(stream)),
+               "cudalm_w4a16_chain_status")
 
 
 # ---------------------------------------------------------------------------

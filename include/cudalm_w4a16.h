@@ -113,6 +113,56 @@ int cudalm_w4a16_gemv_bf16_multi(const cudalm_w4a16_proj* projs, int count,
                                  const uint16_t* x, int K, int M, int prepacked,
                                  hipStream_t stream);
 
+/* Stage chains: an ordered list of projection stages run by ONE persistent
+ * launch, for the dependent projection sequence of a decode step
+ * (src/runtime/qwen35_model.cpp:469-491 issues each projection as its own
+ * launch; src/runtime/qwen35_deltanet.cpp:166-251). No counterpart in the
+ * reference. A stage is up to 4 projections sharing x[M, K] (as in
+ * cudalm_w4a16_gemv_bf16_multi); `dep` names an earlier stage (or -1) that
+ * must have completed before this stage reads x, because x is that stage's
+ * output or simply must follow it. A stage that writes a buffer another
+ * stage reads must depend (directly or through deps) on every such reader.
+ * Each output has the bits cudalm_w4a16_gemv_bf16 gives on the same inputs.
+ * Limits: 1 <= M <= 32, K % 128 == 0 and K <= 4096, 1..4 projections per
+ * stage, up to CUDALM_W4A16_MAX_STAGES stages; x and (prepacked) weights
+ * 16 B aligned, y and scales 2 B aligned.
+ *
+ * The workspace is caller-owned device memory of
+ * cudalm_w4a16_chain_workspace_bytes(n) bytes, 256 B aligned, holding the
+ * plan, the completion flags and counters; one workspace serves one chain,
+ * and launches sharing a workspace must not overlap in time.
+ * cudalm_w4a16_chain_plan validates the stages, writes the plan into the
+ * workspace and synchronizes `stream` (set-up time; not capturable);
+ * cudalm_w4a16_chain_run is one kernel launch with no other stream work,
+ * so it may be captured into a HIP graph and replayed. Every wait inside the
+ * launch is bounded: on a timeout the chain finishes with unspecified
+ * outputs and cudalm_w4a16_chain_status reports CUDALM_W4A16_ETIMEOUT. */
+#define CUDALM_W4A16_MAX_STAGES 256
+#define CUDALM_W4A16_ETIMEOUT (-10) /* a chain stage's wait passed its bound */
+typedef struct cudalm_w4a16_stage {
+  const cudalm_w4a16_proj* projs; /* 1..4 projections reading x */
+  int count;
+  const uint16_t* x; /* bf16 [M, K] */
+  int K;
+  int dep; /* earlier stage that must complete before x is read, or -1 */
+} cudalm_w4a16_stage;
+typedef struct cudalm_w4a16_chain { /* filled by cudalm_w4a16_chain_plan */
+  void* workspace;
+  int n_stages, M, prepacked, grid, gt_max;
+} cudalm_w4a16_chain;
+size_t cudalm_w4a16_chain_workspace_bytes(int n_stages);
+int cudalm_w4a16_chain_plan(const cudalm_w4a16_stage* stages, int n_stages, int M, int prepacked,
+                            void* workspace, size_t workspace_bytes, cudalm_w4a16_chain* chain,
+                            hipStream_t stream);
+int cudalm_w4a16_chain_run(const cudalm_w4a16_chain* chain, hipStream_t stream);
+/* Synchronizes `stream`, then returns CUDALM_W4A16_ETIMEOUT (and clears
+ * the record) if a wait of a run since the last call timed out, else 0. */
+int cudalm_w4a16_chain_status(const cudalm_w4a16_chain* chain, hipStream_t stream);
+/* plan + run in one call (not capturable: the plan synchronizes). */
+int cudalm_w4a16_gemv_bf16_chain(const cudalm_w4a16_stage* stages, int n_stages, int M,
+                                 int prepacked, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream);
+
 /* fp16-activation twin of cudalm_w4a16_gemv_bf16: x and y are fp16 bit
  * patterns, y[m, n] = fp16_rne( sum_k q * f32(scale) * f32(x[m, k]) ) with
  * fp32 accumulation. Replaces int4_gemv (M == 1; include/cudalm/kernels/

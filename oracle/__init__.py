@@ -42,6 +42,7 @@ _SIGS = {
     "orc_gemv_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64], None),
     "orc_gemv_bf16_mt": ([_P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
     "orc_gemv_f64": ([_P, _P, _P, _P, _P, _I64, _I64, _I64], None),
+    "orc_gemv_f32acc_mt": ([_P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
     "orc_gemv_f64_mt": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
     "orc_xorshift32_fill": ([ctypes.c_uint32, _P, ctypes.c_size_t], None),
     "orc_fixture_gemv": ([ctypes.c_uint32, _I64, _I64, _P, _P, _P], None),
@@ -159,6 +160,25 @@ def gemv_bf16(W, S, X, N: int, K: int, M: int = 1, nthreads: int = 1) -> np.ndar
     return Y
 
 
+def gemv_f32acc(W, S, X, N: int, K: int, M: int = 1, nthreads: int = 1) -> np.ndarray:
+    """The fp32 accumulator of ref_gemv_bf16 (tests/cuda/test_int4_gemv_bf16.cpp:
+    54-69) before its bf16 rounding, float32 [M, N]: the fp32-accumulated
+    reference the 2-ulp bar is stated against."""
+    Y = np.empty((M, N), np.float32)
+    _lib.orc_gemv_f32acc_mt(_p(W), _p(S), _p(X), _p(Y), N, K, M, max(1, nthreads))
+    return Y
+
+
+def ulp_vs_fp32_reference(y_bits, acc) -> dict:
+    """Distance of bf16 outputs from the reference loop's fp32 accumulator,
+    in bf16 ulps at the accumulator's magnitude: max and count beyond 2."""
+    acc = np.asarray(acc, np.float64)
+    y = bf16_to_f32(np.asarray(y_bits, np.uint16).reshape(acc.shape)).astype(np.float64)
+    d = np.abs(y - acc) / bf16_ulp(acc)
+    return {"max_ulp_vs_fp32_ref": float(d.max()) if d.size else 0.0,
+            "n_over_2ulp_vs_fp32_ref": int((d > 2.0).sum()), "n": int(d.size)}
+
+
 def gemv_f64(W, S, X, N: int, K: int, M: int = 1, nthreads: int = 1):
     """fp64 sum of the exact fp32 terms and the sum of their magnitudes
     (rows split over `nthreads` threads; the values do not depend on it)."""
@@ -257,6 +277,26 @@ def check_against_reference_loop(y_bits, W, S, X, N, K, M, nthreads: int = 1, sl
     _, sr = check_tolerance_f64(gemv_bf16(W, S, X, N, K, M, nthreads), r, a, M, N)
     st["ref_max_ulp"], st["ref_n_over_2ulp"] = sr["max_ulp"], sr["n_over_2ulp"]
     return ok and st["n_over_2ulp"] <= sr["n_over_2ulp"] + slack, st, sr
+
+
+def full_parity(y_bits, W, S, X, N, K, M, nthreads: int = 1):
+    """Every W4A16 parity figure of one output block, each sum computed once:
+    (ok, stats). ok iff (a) every output is within check_tolerance's bound
+    of the fp64 sum and (b) within 2 bf16 ulps of the reference loop's fp32
+    accumulator plus both fp32 sums' accumulation error (2 * CANCEL_FLOOR *
+    sum|terms|). stats: check_tolerance_f64's figures, the reference loop's
+    ref_max_ulp / ref_n_over_2ulp against the fp64 sum, and
+    ulp_vs_fp32_reference's max / count beyond 2."""
+    r, a = gemv_f64(W, S, X, N, K, M, nthreads)
+    ok, st = check_tolerance_f64(y_bits, r, a, M, N)
+    acc = gemv_f32acc(W, S, X, N, K, M, nthreads)
+    _, sr = check_tolerance_f64(f32_to_bf16(acc), r, a, M, N)
+    st["ref_max_ulp"], st["ref_n_over_2ulp"] = sr["max_ulp"], sr["n_over_2ulp"]
+    st.update(ulp_vs_fp32_reference(y_bits, acc))
+    y = bf16_to_f32(np.asarray(y_bits, np.uint16).reshape(M, N)).astype(np.float64)
+    lim = 2.0 * bf16_ulp(acc) + 2.0 * CANCEL_FLOOR * a
+    st["n_bad_vs_fp32_ref"] = int((~(np.abs(y - acc.astype(np.float64)) <= lim)).sum())
+    return ok and st["n_bad_vs_fp32_ref"] == 0, st
 
 
 def check_tolerance(y_bits, W, S, X, N, K, M, ulps: float = 2.0, nthreads: int = 1):

@@ -206,9 +206,9 @@ int orc_quantize(const float* Wf, int64_t N, int64_t K, uint8_t* Wp,
  * row m (batch_decode.cu:99-105: row m uses x + m*K and writes y + m*N).
  * Per output: fp32 acc, k ascending, lo before hi, each term (q * s) * x,
  * one bf16 RNE store. */
-void orc_gemv_bf16_rows(const uint8_t* W, const uint16_t* S, const uint16_t* X,
-                        uint16_t* Y, int64_t N, int64_t K, int64_t M,
-                        int64_t n_begin, int64_t n_end) {
+static void gemv_acc_rows(const uint8_t* W, const uint16_t* S, const uint16_t* X,
+                          uint16_t* Y, float* Yacc, int64_t N, int64_t K, int64_t M,
+                          int64_t n_begin, int64_t n_end) {
   const int64_t G = K / 128;
   float* xf = (float*)malloc(sizeof(float) * (size_t)K);
   for (int64_t m = 0; m < M; ++m) {
@@ -224,10 +224,17 @@ void orc_gemv_bf16_rows(const uint8_t* W, const uint16_t* S, const uint16_t* X,
         acc += (float)lo * s * xf[2 * b];
         acc += (float)hi * s * xf[2 * b + 1];
       }
-      Y[m * N + n] = orc_f32_to_bf16_rne(acc);
+      if (Y) Y[m * N + n] = orc_f32_to_bf16_rne(acc);
+      if (Yacc) Yacc[m * N + n] = acc;
     }
   }
   free(xf);
+}
+
+void orc_gemv_bf16_rows(const uint8_t* W, const uint16_t* S, const uint16_t* X,
+                        uint16_t* Y, int64_t N, int64_t K, int64_t M,
+                        int64_t n_begin, int64_t n_end) {
+  gemv_acc_rows(W, S, X, Y, NULL, N, K, M, n_begin, n_end);
 }
 
 void orc_gemv_bf16(const uint8_t* W, const uint16_t* S, const uint16_t* X,
@@ -241,21 +248,21 @@ typedef struct {
   const uint16_t* X;
   uint16_t* Y;
   int64_t N, K, M, n0, n1;
+  float* Yacc;
 } orc_job;
 
 static void* orc_job_run(void* p) {
   orc_job* j = (orc_job*)p;
-  orc_gemv_bf16_rows(j->W, j->S, j->X, j->Y, j->N, j->K, j->M, j->n0, j->n1);
+  gemv_acc_rows(j->W, j->S, j->X, j->Y, j->Yacc, j->N, j->K, j->M, j->n0, j->n1);
   return NULL;
 }
 
 /* Same arithmetic, output rows partitioned over threads (bit-identical to
  * the single-thread call: every output keeps its own sequential k loop). */
-void orc_gemv_bf16_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X,
-                      uint16_t* Y, int64_t N, int64_t K, int64_t M,
-                      int nthreads) {
+static void gemv_acc_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y,
+                        float* Yacc, int64_t N, int64_t K, int64_t M, int nthreads) {
   if (nthreads <= 1 || N < 2) {
-    orc_gemv_bf16(W, S, X, Y, N, K, M);
+    gemv_acc_rows(W, S, X, Y, Yacc, N, K, M, 0, N);
     return;
   }
   if (nthreads > 256) nthreads = 256;
@@ -268,11 +275,25 @@ void orc_gemv_bf16_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X,
     int64_t n1 = n0 + per;
     if (n0 >= N) break;
     if (n1 > N) n1 = N;
-    jobs[t] = (orc_job){W, S, X, Y, N, K, M, n0, n1};
+    jobs[t] = (orc_job){W, S, X, Y, N, K, M, n0, n1, Yacc};
     pthread_create(&th[t], NULL, orc_job_run, &jobs[t]);
     ++used;
   }
   for (int t = 0; t < used; ++t) pthread_join(th[t], NULL);
+}
+
+void orc_gemv_bf16_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X,
+                      uint16_t* Y, int64_t N, int64_t K, int64_t M,
+                      int nthreads) {
+  gemv_acc_mt(W, S, X, Y, NULL, N, K, M, nthreads);
+}
+
+/* The same loop's fp32 accumulator before its bf16 rounding: the
+ * "fp32-accumulated reference" a kernel output is measured against in bf16
+ * ulps. orc_gemv_bf16 == bf16_rne(orc_gemv_f32acc) bit for bit. */
+void orc_gemv_f32acc_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X,
+                        float* Yacc, int64_t N, int64_t K, int64_t M, int nthreads) {
+  gemv_acc_mt(W, S, X, NULL, Yacc, N, K, M, nthreads);
 }
 
 /* ref_gemv of tests/cuda/test_int4_gemv.cpp:49-63 (fp16 activations and

@@ -23,6 +23,8 @@
  *   orc_gemv_bf16        brute-force fp32 sequential loop in numpy for tiny
  *                        shapes (bit-exact), fp64 matmul bound at all shapes,
  *                        closed forms (zero row, one-hot x, linearity, sign)
+ *   orc_gemv_f32acc_mt   brute-force fp32 accumulator in numpy (bit-exact) and
+ *                        bf16_rne of it == orc_gemv_bf16 at every test shape
  *   orc_gemv_f64         numpy float64 matmul of the dequantized weights
  *   orc_gemv_f16         as orc_gemv_bf16, with numpy float16 activations and
  *                        output (brute force bit-exact, fp64 bound, closed
@@ -66,6 +68,8 @@ void orc_gemv_bf16_rows(const uint8_t* W, const uint16_t* S, const uint16_t* X,
 void orc_gemv_bf16_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X,
                       uint16_t* Y, int64_t N, int64_t K, int64_t M,
                       int nthreads);
+void orc_gemv_f32acc_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X,
+                        float* Yacc, int64_t N, int64_t K, int64_t M, int nthreads);
 void orc_gemv_f64_mt(const uint8_t* W, const uint16_t* S, const uint16_t* X, double* Y,
                      double* Yabs, int64_t N, int64_t K, int64_t M, int nthreads);
 void orc_gemv_f64(const uint8_t* W, const uint16_t* S, const uint16_t* X,

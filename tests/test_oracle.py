@@ -169,8 +169,8 @@ def test_quantizer_rejects_bad_input(orc):
 
 # ---------------------------------------------------------------- gemv ------
 
-def _numpy_sequential_gemv(W, S, X, N, K):
-    """fp32, k ascending, lo before hi, each term (q*s)*x, then bf16 RNE."""
+def _numpy_sequential_acc(W, S, X, N, K):
+    """fp32 accumulator, k ascending, lo before hi, each term (q*s)*x."""
     f32 = np.float32
     out = np.empty(N, np.float32)
     xs = (X.astype(np.uint32) << 16).view(np.float32).ravel()
@@ -184,6 +184,12 @@ def _numpy_sequential_gemv(W, S, X, N, K):
             acc = f32(acc + f32(f32(f32(lo) * s) * xs[2 * b]))
             acc = f32(acc + f32(f32(f32(hi) * s) * xs[2 * b + 1]))
         out[n] = acc
+    return out
+
+
+def _numpy_sequential_gemv(W, S, X, N, K):
+    """The same, then bf16 RNE."""
+    out = _numpy_sequential_acc(W, S, X, N, K)
     return torch.from_numpy(out).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
 
 
@@ -192,6 +198,38 @@ def test_gemv_bruteforce_bitexact(orc, N, K, seed):
     W, S, X = orc.fixture_gemv(seed, N, K)
     y = orc.gemv_bf16(W, S, X, N, K, 1)[0]
     assert np.array_equal(y, _numpy_sequential_gemv(W, S, X, N, K))
+
+
+@pytest.mark.parametrize("N,K,seed", [(1, 128, 1), (3, 128, 0x51ed), (5, 256, 9), (2, 384, 77)])
+def test_gemv_f32acc_bruteforce_bitexact(orc, N, K, seed):
+    """The fp32-accumulated reference: the loop's accumulator, bit for bit."""
+    W, S, X = orc.fixture_gemv(seed, N, K)
+    acc = orc.gemv_f32acc(W, S, X, N, K, 1)[0]
+    assert np.array_equal(acc.view(np.uint32), _numpy_sequential_acc(W, S, X, N, K).view(np.uint32))
+
+
+@pytest.mark.parametrize("N,K,M", [(37, 256, 3), (64, 1024, 1), (16, 3584, 2), (1000, 1024, 4)])
+def test_gemv_f32acc_rounds_to_reference(orc, N, K, M):
+    """bf16_rne(accumulator) is the reference loop's output at every shape,
+    single- and multi-threaded; ulp_vs_fp32_reference of the loop's own
+    output is at most 0.5 ulp (one rounding), and a one-ulp shift of every
+    output is seen as 0.5 to 1.5 ulp (2.5 where the output crosses a power
+    of two: a step above it is two ulps of an accumulator just below it)."""
+    W, S, _ = orc.fixture_gemv(N * 7 + K, N, K)
+    X = orc.synth_act(N + K + M, M, K)
+    acc1 = orc.gemv_f32acc(W, S, X, N, K, M, 1)
+    acc8 = orc.gemv_f32acc(W, S, X, N, K, M, 8)
+    assert np.array_equal(acc1.view(np.uint32), acc8.view(np.uint32))
+    y = orc.gemv_bf16(W, S, X, N, K, M)
+    assert np.array_equal(orc.f32_to_bf16(acc1), y)
+    st = orc.ulp_vs_fp32_reference(y, acc1)
+    assert st["max_ulp_vs_fp32_ref"] <= 0.5 + 1e-9 and st["n_over_2ulp_vs_fp32_ref"] == 0
+    # move every nonzero output one bf16 step away from zero: 0.5..1.5 ulp
+    nz = (y & 0x7FFF) != 0
+    y2 = np.where(nz & ((y & 0x7F80) != 0x7F80), y + 1, y).astype(np.uint16)
+    st2 = orc.ulp_vs_fp32_reference(y2, acc1)
+    assert 0.5 <= st2["max_ulp_vs_fp32_ref"] <= 2.5 + 1e-9
+    assert st2["n_over_2ulp_vs_fp32_ref"] <= nz.sum() // 50
 
 
 @pytest.mark.parametrize("N,K", [(37, 256), (64, 1024), (16, 3584)])
