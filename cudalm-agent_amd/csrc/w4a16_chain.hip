@@ -63,6 +63,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 #include <vector>
 
@@ -472,6 +473,10 @@ int chain_launch(int prepacked, uint8_t* ws, int nst, int M, int gt, int* grid_o
   return chain_launch_t<false, 4, 2>(ws, nst, M, gt, grid_or_occ, launch, stream);
 }
 
+int chain_plan_into(const cudalm_w4a16_stage* stages, int n_stages, int M, int prepacked,
+                    void* workspace, size_t workspace_bytes, cudalm_w4a16_chain* chain,
+                    hipStream_t stream, ChainStage* tab);
+
 }  // namespace
 
 extern "C" {
@@ -484,13 +489,51 @@ size_t cudalm_w4a16_chain_workspace_bytes(int n_stages) {
 int cudalm_w4a16_chain_plan(const cudalm_w4a16_stage* stages, int n_stages, int M, int prepacked,
                             void* workspace, size_t workspace_bytes, cudalm_w4a16_chain* chain,
                             hipStream_t stream) {
+  if (n_stages < 1 || n_stages > CUDALM_W4A16_MAX_STAGES) return CUDALM_W4A16_EINVAL;
+  std::vector<ChainStage> tab(static_cast<size_t>(n_stages));
+  return chain_plan_into(stages, n_stages, M, prepacked, workspace, workspace_bytes, chain, stream,
+                         tab.data());
+}
+
+}  // extern "C"
+
+namespace {
+
+// Allocation-free chains (cudalm_w4a16_gemv_bf16_chain_noalloc): the plan,
+// flags and counters live in this file-scope device array, one copy per
+// GPU, up to kChainStaticStages stages. Host code never uses the array's
+// name as an address: the device address comes from hipGetSymbolAddress,
+// looked up once per device with that device current, and is what every
+// copy, memset and kernel argument uses.
+constexpr int kChainStaticStages = 128;
+constexpr size_t kChainStaticBytes =
+    kChainHeader + static_cast<size_t>(kChainStaticStages) * sizeof(ChainStage) +
+    static_cast<size_t>(kChainStaticStages) * kChainFlagSlots * kChainFlagStride * 4;
+static __device__ __align__(256) uint8_t scratch[kChainStaticBytes];
+
+void* scratch_ptr() {
+  static std::atomic<void*> ptrs[kMaxDevices];
+  const int dev = current_device();
+  if (dev < 0) return nullptr;
+  void* p = ptrs[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return nullptr;
+    ptrs[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
+// The plan, written into `workspace` from the host table `tab` (n_stages
+// entries, filled here).
+int chain_plan_into(const cudalm_w4a16_stage* stages, int n_stages, int M, int prepacked,
+                    void* workspace, size_t workspace_bytes, cudalm_w4a16_chain* chain,
+                    hipStream_t stream, ChainStage* tab) {
   if (!stages || !workspace || !chain) return CUDALM_W4A16_ENULL;
   if (n_stages < 1 || n_stages > CUDALM_W4A16_MAX_STAGES || M < 1 || M > 32)
     return CUDALM_W4A16_EINVAL;
   const size_t need = cudalm_w4a16_chain_workspace_bytes(n_stages);
   if (workspace_bytes < need) return CUDALM_W4A16_EINVAL;
   if (!aligned(workspace, 256)) return CUDALM_W4A16_EALIGN;
-  std::vector<ChainStage> tab(static_cast<size_t>(n_stages));
   int gt_max = 0;  // max tpw * G over stages
   for (int s = 0; s < n_stages; ++s) {
     const cudalm_w4a16_stage& st = stages[s];
@@ -550,7 +593,7 @@ int cudalm_w4a16_chain_plan(const cudalm_w4a16_stage* stages, int n_stages, int 
   }
   // header and flags zeroed, then the stage table
   if (hipMemsetAsync(workspace, 0, need, stream) != hipSuccess) return CUDALM_W4A16_ELAUNCH;
-  if (hipMemcpyAsync(static_cast<uint8_t*>(workspace) + kChainHeader, tab.data(),
+  if (hipMemcpyAsync(static_cast<uint8_t*>(workspace) + kChainHeader, tab,
                      chain_table_bytes(n_stages), hipMemcpyHostToDevice, stream) != hipSuccess)
     return CUDALM_W4A16_ELAUNCH;
   if (hipStreamSynchronize(stream) != hipSuccess) return CUDALM_W4A16_ELAUNCH;
@@ -562,6 +605,10 @@ int cudalm_w4a16_chain_plan(const cudalm_w4a16_stage* stages, int n_stages, int 
   chain->gt_max = gt_max;
   return CUDALM_W4A16_OK;
 }
+
+}  // namespace
+
+extern "C" {
 
 int cudalm_w4a16_chain_run(const cudalm_w4a16_chain* chain, hipStream_t stream) {
   if (!chain || !chain->workspace) return CUDALM_W4A16_ENULL;
@@ -591,6 +638,20 @@ int cudalm_w4a16_gemv_bf16_chain(const cudalm_w4a16_stage* stages, int n_stages,
   cudalm_w4a16_chain chain;
   if (int rc = cudalm_w4a16_chain_plan(stages, n_stages, M, prepacked, workspace, workspace_bytes,
                                        &chain, stream))
+    return rc;
+  return cudalm_w4a16_chain_run(&chain, stream);
+}
+
+int cudalm_w4a16_gemv_bf16_chain_noalloc(const cudalm_w4a16_stage* stages, int n_stages, int M,
+                                         int prepacked, hipStream_t stream) {
+  if (n_stages > kChainStaticStages) return CUDALM_W4A16_ERANGE;
+  if (n_stages < 1) return CUDALM_W4A16_EINVAL;
+  void* ws = scratch_ptr();
+  if (ws == nullptr) return CUDALM_W4A16_ELAUNCH;
+  ChainStage tab[kChainStaticStages];  // host copy of the plan, on the stack
+  cudalm_w4a16_chain chain;
+  if (int rc = chain_plan_into(stages, n_stages, M, prepacked, ws, kChainStaticBytes, &chain, stream,
+                               tab))
     return rc;
   return cudalm_w4a16_chain_run(&chain, stream);
 }

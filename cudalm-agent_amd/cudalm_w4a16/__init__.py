@@ -74,6 +74,7 @@ _SIGS = {
     "cudalm_w4a16_chain_run": ([_P, _P], _I),
     "cudalm_w4a16_chain_status": ([_P, _P], _I),
     "cudalm_w4a16_gemv_bf16_chain": ([_P, _I, _I, _I, _P, _SZ, _P], _I),
+    "cudalm_w4a16_gemv_bf16_chain_noalloc": ([_P, _I, _I, _I, _P], _I),
 }
 for _name, (_args, _ret) in _SIGS.items():
     _fn = getattr(_lib, _name)

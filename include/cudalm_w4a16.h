@@ -163,6 +163,21 @@ int cudalm_w4a16_gemv_bf16_chain(const cudalm_w4a16_stage* stages, int n_stages,
                                  int prepacked, void* workspace, size_t workspace_bytes,
                                  hipStream_t stream);
 
+/* cudalm_w4a16_gemv_bf16_chain without a caller workspace, for callers that
+ * cannot allocate device memory (code under graph-capture set-up, tight
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The plan, flags and counters live in a file-scope device array
+ * of the library (4,228,096 bytes per GPU, held until the process ends) that
+ * holds up to CUDALM_W4A16_NOALLOC_MAX_STAGES stages; more stages return
+ * CUDALM_W4A16_ERANGE. The call allocates nothing (no hipMalloc, no device
+ * allocation of any library); it plans (copying the plan into that array and
+ * synchronizing `stream`) and launches. Every call on one GPU shares that
+ * GPU's array: calls that overlap in time on one GPU race, so serialize
+ * them. Same limits and outputs as cudalm_w4a16_gemv_bf16_chain. */
+#define CUDALM_W4A16_NOALLOC_MAX_STAGES 128
+int cudalm_w4a16_gemv_bf16_chain_noalloc(const cudalm_w4a16_stage* stages, int n_stages, int M,
+                                         int prepacked, hipStream_t stream);
+
 /* fp16-activation twin of cudalm_w4a16_gemv_bf16: x and y are fp16 bit
  * patterns, y[m, n] = fp16_rne( sum_k q * f32(scale) * f32(x[m, k]) ) with
  * fp32 accumulation. Replaces int4_gemv (M == 1; include/cudalm/kernels/
