@@ -203,10 +203,8 @@ int stream_rows_per_chunk(int K, int M) {
   return mc;
 }
 
-int stream_wgs_per_cu() {
-  static const int occ = env_setting("CUDALM_BF16_GEMV_WGS_PER_CU", 4, 1, 32);
-  return occ;
-}
+// resident workgroups per CU of the persistent bf16 stream kernel
+int stream_wgs_per_cu() { return 4; }
 
 template <int CT, bool PACKED = false>
 int launch_stream_ct(const uint16_t* W, const uint16_t* X, uint16_t* Y, int N, int K, int M,

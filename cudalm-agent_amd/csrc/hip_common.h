@@ -107,15 +107,6 @@ bool allow_lds(F kernel, size_t bytes) {
                              static_cast<int>(kLdsMax)) == hipSuccess;
 }
 
-// Integer setting from the environment, read once (thread-safe static
-// initialization); `fallback` when unset or outside [lo, hi].
-inline int env_setting(const char* name, int fallback, int lo, int hi) {
-  const char* e = getenv(name);
-  if (!e) return fallback;
-  const int v = atoi(e);
-  return (v >= lo && v <= hi) ? v : fallback;
-}
-
 template <typename F>
 int regs_of(F kernel) {
   hipFuncAttributes attr;

@@ -80,16 +80,14 @@ __device__ __forceinline__ f32x4_t group_offset(const u32x4_t (&xa)[4]) {
   return c;
 }
 
-// Prefill-chunk GEMM (M >= 33) in w4a16_gemm.hip. cfg < 0 picks the tile
-// shape by problem size; other values force one (measurement only). Returns
-// a CUDALM_W4A16_* code, or 1 when cfg names no configuration of this
-// kernel (the caller then uses its own).
+// Prefill-chunk GEMM on 32 x 32 MFMA tiles (w4a16_gemm.hip): 32 activation
+// rows x 256 weight rows per 8-wave workgroup, any M, N and K % 128 == 0.
 template <bool PACKED>
-int launch_prefill_group(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
-                         int K, int M, int cfg, hipStream_t stream);
+int launch_prefill32(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
+                     int K, int M, hipStream_t stream);
 
-// Registers per lane of the default prefill GEMM instance.
-int prefill_group_regs();
+// Registers per lane of that kernel (prepacked instance).
+int prefill32_regs();
 
 }  // namespace cudalm_hip
 

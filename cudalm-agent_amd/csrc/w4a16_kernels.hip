@@ -483,71 +483,6 @@ __device__ __forceinline__ float* stream_prologue(u32x4_t* xs, const u32x4_t* (&
   return corr;
 }
 
-// Stream kernel: M <= 16 * CT, all of x resident in LDS; waves stream
-// 16-row weight tiles of every projection in P (grid-stride) in units of
-// up to 8 groups, prefetching the next unit while the current one is
-// multiplied. NR = accumulator rows per lane that can hold outputs (1 when
-// M == 1, else 4).
-template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
-__global__ __launch_bounds__(kStreamWaves * 64) void w4a16_stream_kernel(
-    const ProjTable P, const uint16_t* __restrict__ X, int K, int M) {
-  extern __shared__ u32x4_t xs[];
-  const int G = K >> 7;
-  const int lane = threadIdx.x & 63;
-  const int wave = wave_id();
-  const int i = lane & 15, a = lane >> 4;
-  const int ntiles = P.ntiles;
-  const int U = (G + kUnit - 1) / kUnit;
-  const int stride = gridDim.x * kStreamWaves;
-  int t = blockIdx.x * kStreamWaves + wave;
-  const bool active = t < ntiles;
-
-  // x's first batch, then the first unit's weights, fly together
-  StageBatch sb0;
-  stage_load(sb0, X, K, 0, M, 0, K, 0);
-  StreamUnit cur, nxt;
-  stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t, ntiles - 1), 0, lane);
-  const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT, Act>(xs, xrow, X, K, M, wave, i, a, sb0);
-  if (!active) return;
-
-  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f32x4_t part[CT], total[CT];
-#pragma unroll
-  for (int ct = 0; ct < CT; ++ct) part[ct] = total[ct] = zero;
-  int u = 0;
-  while (true) {
-    int nt = t, nu = u + 1;
-    if (nu == U) {
-      nu = 0;
-      nt = t + stride;
-    }
-    const bool has_next = nt < ntiles;
-    // past the last unit, re-read the current one instead of branching
-    // around the loads (with the non-temporal weight loads this re-read
-    // goes to HBM; this whole-unit kernel is kept as a measurement
-    // baseline, the piece kernel reads a sink there)
-    stream_load_t<PACKED, SVEC>(nxt, P, K, G, has_next ? nt : t, has_next ? nu * kUnit : u * kUnit,
-                                lane);
-    const int g0 = u * kUnit;
-    stream_unit<NR, CT, Layout<Act, PACKED>>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      total[ct] = total[ct] + part[ct];
-      part[ct] = zero;
-    }
-    if (u == U - 1) {
-      store_tile<NR, CT, Act>(P, t, total, M, i, a);
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
-    }
-    if (!has_next) break;
-    cur = nxt;
-    t = nt;
-    u = nu;
-  }
-}
-
 // Read-only target of the stream kernel's last, unused piece load: 4 KB of
 // piece plus the lane spread, never written. Pointing that load here keeps
 // the loop's loads unconditional (a conditional load makes the compiler
@@ -1015,15 +950,6 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
 // SwiGLU; P holds gate then up with equal N, row tile t is gate tile t and
 // up tile nt + t, and the output is silu(gate) * up on the bf16-rounded
 // projections (blockIdx.y walks chunks of mc activation rows).
-#ifdef CUDALM_SPLIT_PROBE
-// measurement build only: per-wave phase timestamps (s_memrealtime, 100 MHz)
-__device__ unsigned long long g_split_probe[4096 * 16 * 8];
-#define SPLIT_PROBE(k)                                                         \
-  if (lane == 0 && blockIdx.x < 4096 && blockIdx.y == 0)                       \
-  g_split_probe[(blockIdx.x * 16 + wave) * 8 + (k)] = __builtin_amdgcn_s_memrealtime()
-#else
-#define SPLIT_PROBE(k)
-#endif
 
 template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, int NP = 1,
           bool DX = false, class PT = ProjTable>
@@ -1036,7 +962,6 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   const int i = lane & 15, a = lane >> 4;
-  SPLIT_PROBE(0);
   const int nt = NP == 1 ? P.ntiles : P.tile_end[0];  // row tiles
   const int U = (G + kUnit - 1) / kUnit;
   const int H = (G + HG - 1) / HG;  // pieces of a tile that hold groups
@@ -1074,7 +999,6 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
                                                G, h * HG);
   };
   load_slot(min(wave, nslots - 1));
-  SPLIT_PROBE(1);
   const u32x4_t* xrow[CT];
   const float* corr = nullptr;
   if constexpr (!DX) corr = stream_prologue<CT, Act, true>(xs, xrow, Xc, K, mrows, wave, i, a, sb0);
@@ -1128,9 +1052,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
       }
     }
   }
-  SPLIT_PROBE(2);
   __syncthreads();
-  SPLIT_PROBE(3);
   if (wave < TPR && t0 + wave < nt) {
     f32x4_t total[NP][CT];
 #pragma unroll
@@ -1170,10 +1092,8 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
         for (int ct = 0; ct < CT; ++ct) total[pj][ct] = total[pj][ct] + p[ct];
       }
     }
-    SPLIT_PROBE(4);
     if constexpr (NP == 1) {
       store_tile<NR, CT, Act, PT>(P, t0 + wave, total[0], M, i, a);
-      SPLIT_PROBE(5);
     } else {
       const int N = P.n[0];
       const int n = (t0 + wave) * kTileRows + i;
@@ -1363,15 +1283,6 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
   const int tid = static_cast<int>(threadIdx.x) - slice * NT;
   const int i = lane & 15, a = lane >> 4;
   const int m0 = blockIdx.y * TM;
-#ifdef CUDALM_SPLIT_PROBE
-  const int wave_p = wave_id();
-#define UNIT_PROBE(k)                                                                  \
-  if (lane == 0 && blockIdx.x < 256 && blockIdx.y < 16 && wave_p < 16)                 \
-  g_split_probe[((blockIdx.y * 256 + blockIdx.x) * 16 + wave_p) * 8 + (k)] = __builtin_amdgcn_s_memrealtime()
-#else
-#define UNIT_PROBE(k)
-#endif
-  UNIT_PROBE(0);
   const int mrows = min(TM, M - m0);
   u32x4_t* xs = lds + slice * XB;
   float* corr = reinterpret_cast<float*>(lds + KS * XB) + slice * (kUnit * CT * 16);
@@ -1450,14 +1361,12 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
       }
     }
     if (it > 0) __syncthreads();  // previous unit's readers are done
-    UNIT_PROBE(1);
     {
       u32x4_t* xdst = xs + r0 * PB + b;
 #pragma unroll
       for (int q = 0; q < BPT; ++q) xdst[q * RS * PB] = pair_order(v[q]);
     }
     __syncthreads();
-    UNIT_PROBE(2);
     // offset table of the unit: chains (group, column tile) split over waves
     // (IOFF: each wave runs the chains of its own groups inline instead, the
     // same operands, and the table and its barrier are skipped)
@@ -1471,7 +1380,6 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
       }
       __syncthreads();
     }
-    UNIT_PROBE(3);
     if (!any_ok) continue;
 
     f32x4_t part[RB][CT];
@@ -1524,7 +1432,6 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) acc[0][rb][ct] = acc[0][rb][ct] + part[rb][ct];
-      UNIT_PROBE(4);
     } else {
 #pragma unroll
       for (int q = 0; q < NPART; ++q)
@@ -1583,7 +1490,6 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
           col[static_cast<size_t>(ct * 16 + r) * N] =
               static_cast<uint16_t>(f32_to_bf16_rne(16.0f * total[rb][ct][r]));
   }
-  UNIT_PROBE(5);
 }
 
 // ---------------------------------------------------------------------------
@@ -1742,52 +1648,13 @@ size_t split_lds_bytes(int K, int M) {
 
 bool split_fits(int K, int M) { return M <= 32 && split_lds_bytes(K, M) <= kLdsMax; }
 
-// Stream-kernel fetch granularity (CUDALM_W4A16_STREAM_PIECE, measurement
-// only): 1 = pieces of 4 groups (default), 2 = pieces of 2 groups, 0 = whole
-// 8-group units. Same bits in every mode.
-int stream_half_enabled() {
-  static const int v = env_setting("CUDALM_W4A16_STREAM_PIECE", 1, 0, 2);
-  return v;
-}
-
-int stream_occupancy() {
-  static const int occ = env_setting("CUDALM_W4A16_STREAM_WGS_PER_CU", 3, 1, 32);
-  return occ;
-}
-
-// Share of the tiles (per mille) left to dispatcher-balanced workgroups
-// after the persistent ones (CUDALM_W4A16_STREAM_TAIL, measurement only;
-// 0 = all static, the default).
-int stream_tail_permille() {
-  static const int v = env_setting("CUDALM_W4A16_STREAM_TAIL", 0, 0, 900);
-  return v;
-}
-
-// Single-projection launches pass a 40-byte argument struct (ProjOne)
-// instead of the 264-byte table (CUDALM_W4A16_PROJ_ONE, measurement only:
-// 0 = the full table).
-int proj_one_enabled() {
-  static const int v = env_setting("CUDALM_W4A16_PROJ_ONE", 1, 0, 1);
-  return v;
-}
-
-// Workgroups per CU of the 8-wave stream kernel (two column tiles).
-// Waves per workgroup of the pair stream kernel (0 = off), and resident
-// workgroups per CU (measurement overrides).
-int stream_pair_waves() {
-  static const int v = env_setting("CUDALM_W4A16_STREAM_PAIR", 8, 0, 8);
-  return v == 4 || v == 8 ? v : 0;
-}
-
-int stream_pair_wgs_per_cu() {
-  static const int v = env_setting("CUDALM_W4A16_STREAM_PAIR_WGS_PER_CU", 1, 1, 4);
-  return v;
-}
-
-int stream_occupancy_wide() {
-  static const int occ = env_setting("CUDALM_W4A16_STREAM_WIDE_WGS_PER_CU", 2, 1, 8);
-  return occ;
-}
+// Resident workgroups per CU of the persistent stream kernels: 3 of the
+// 4-wave one-column-tile kernel, 2 of the 8-wave two-column-tile kernel, 1
+// of the 8-wave pair kernel (measured best on the LM head; the alternatives
+// are recorded in the design notes).
+constexpr int kStreamWgsPerCu = 3;
+constexpr int kStreamWideWgsPerCu = 2;
+constexpr int kPairWaves = 8;
 
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
@@ -1797,82 +1664,50 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   constexpr int WV = CT == 2 ? 8 : kStreamWaves;
   const size_t lds = stream_lds_bytes(K, M);
   const int ntiles = P.ntiles;
-  int per_cu = CT == 2 ? stream_occupancy_wide() : stream_occupancy();
+  int per_cu = CT == 2 ? kStreamWideWgsPerCu : kStreamWgsPerCu;
   const int lds_fit = static_cast<int>(kLdsMax / (lds > 0 ? lds : 1));
   if (lds_fit < per_cu) per_cu = lds_fit > 0 ? lds_fit : 1;
   // Persistent: as many workgroups as stay resident (a tile-count-balanced
   // grid with fewer waves, or one with more than fit, both measured slower
   // on the LM head than this one-round-uneven split).
   const int G = K / kGroup;
-  const int mode = stream_half_enabled();
-  if (mode == 0) {  // whole-unit kernel (measurement baseline), 4-wave workgroups
-    const int want = (ntiles + kStreamWaves - 1) / kStreamWaves;
-    const int cap = cu_count() * per_cu;
-    auto kern = w4a16_stream_kernel<PACKED, NR, SVEC, CT, Act>;
-    if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-    hipLaunchKernelGGL(kern, dim3(want < cap ? want : cap), dim3(kStreamWaves * 64), lds, stream,
-                       P, X, K, M);
-    return launch_status();
-  }
   const int want = (ntiles + WV - 1) / WV;
   const int cap = cu_count() * per_cu;
-  const int pwg = want < cap ? want : cap;
-  int t_static = ntiles, grid = pwg;
-  // Tail workgroups (off by default): the last share of the tiles goes to
-  // one-tile-per-wave workgroups beyond the persistent grid. With cached
-  // weight loads a 15% tail gained 1.4 us on the LM head at M = 1; with
-  // the non-temporal weight loads the all-static grid is faster (M = 1
-  // 23.12 -> 22.84 us, M = 8 25.28 -> 24.60 us against a 15% tail).
-  const int tail_pm = M <= 8 ? stream_tail_permille() : 0;
-  const int tail = static_cast<int>(static_cast<long long>(ntiles) * tail_pm / 1000);
-  if (tail > 0 && ntiles - tail > pwg * WV) {
-    t_static = ntiles - tail;
-    grid = pwg + (tail + WV - 1) / WV;
-  }
+  const int grid = want < cap ? want : cap;
   // Waves with at most one tile compute their offset chains inline and
   // skip the workgroup's offset table and its barrier (3584x1024 M=1:
   // 4.30 -> 4.10 us); waves that stream many tiles share the table (inline
   // chains cost the LM head 0.9 us at M = 1 and 3.6 us at M = 8).
-  const bool ioff = t_static == ntiles && ntiles <= pwg * WV;
-  // two column tiles of one projection: the pair kernel (CUDALM_W4A16_STREAM_PAIR,
-  // 1 = on, the default; 0 = the one-tile kernel, for measurement)
+  const bool ioff = ntiles <= grid * WV;
+  // two column tiles of one projection: the pair kernel, 8 waves, one
+  // workgroup per CU
   if constexpr (CT == 2) {
-    if (P.count == 1 && proj_one_enabled() && stream_pair_waves() > 0 && mode == 1) {
+    if (P.count == 1) {
       const ProjOne one = shrink_table<1>(P);
-      const int wv = stream_pair_waves();
       const int npairs = (ntiles + 1) / 2;
-      auto launch_pair = [&](auto kern, int WVv) {
-        if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-        const int fit = lds_fit > 0 ? lds_fit : 1;
-        const int cap = cu_count() * (fit < stream_pair_wgs_per_cu() ? fit : stream_pair_wgs_per_cu());
-        const int want = (npairs + WVv - 1) / WVv;
-        hipLaunchKernelGGL(kern, dim3(want < cap ? want : cap), dim3(WVv * 64), lds, stream, one, X,
-                           K, M);
-        return launch_status();
-      };
-      if (wv == 4)
-        return G % 4 == 0 ? launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, true, 4, ProjOne>, 4)
-                          : launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, false, 4, ProjOne>, 4);
-      return G % 4 == 0 ? launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, true, 8, ProjOne>, 8)
-                        : launch_pair(w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, false, 8, ProjOne>, 8);
+      auto kern = G % 4 == 0
+                      ? w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, true, kPairWaves, ProjOne>
+                      : w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, false, kPairWaves, ProjOne>;
+      if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+      const int pwant = (npairs + kPairWaves - 1) / kPairWaves;
+      const int pcap = cu_count();
+      hipLaunchKernelGGL(kern, dim3(pwant < pcap ? pwant : pcap), dim3(kPairWaves * 64), lds, stream,
+                         one, X, K, M);
+      return launch_status();
     }
   }
   auto go = [&](const auto& T) {
     using PT = std::decay_t<decltype(T)>;
     auto kern =
-        mode == 2
-            ? (G % 2 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, true, WV, false, PT>
-                          : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 2, false, WV, false, PT>)
-        : ioff
-            ? (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, true, PT>
-                          : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, true, PT>)
-            : (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, false, PT>
-                          : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, false, PT>);
+        ioff ? (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, true, PT>
+                           : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, true, PT>)
+             : (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, false, PT>
+                           : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, false, PT>);
     if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, T, X, K, M, pwg, t_static);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, T, X, K, M, grid, ntiles);
     return launch_status();
   };
-  if (P.count == 1 && proj_one_enabled()) {
+  if (P.count == 1) {
     const ProjOne one = shrink_table<1>(P);
     return go(one);
   }
@@ -1972,13 +1807,13 @@ template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
   const SplitPlan plan = split_piece_plan(P.ntiles, K, M);
   if (plan.hg != 0) {
-    if (P.count == 1 && proj_one_enabled()) {
+    if (P.count == 1) {
       const ProjOne one = shrink_table<1>(P);
       return launch_split_piece<PACKED, NR, SVEC, CT, Act>(one, X, K, M, plan, stream);
     }
     if constexpr (std::is_same<Act, ActBf16>::value) {
       // the fused projection groups (qkv/z/b/a, q/k/v, gate/up) have <= 4
-      if (P.count <= 4 && proj_one_enabled()) {
+      if (P.count <= 4) {
         const ProjFour four = shrink_table<4>(P);
         return launch_split_piece<PACKED, NR, SVEC, CT, Act>(four, X, K, M, plan, stream);
       }
@@ -1989,7 +1824,7 @@ int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStrea
   const int ntiles = P.ntiles;
   const int tpr = split_tiles_per_round(K);
   const int grid = (ntiles + tpr - 1) / tpr;
-  if (P.count == 1 && proj_one_enabled()) {
+  if (P.count == 1) {
     const ProjOne one = shrink_table<1>(P);
     auto kern = w4a16_split_kernel<PACKED, NR, SVEC, CT, Act, ProjOne>;
     if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
@@ -2190,45 +2025,34 @@ int launch_gemm_unit(const uint8_t* W, const uint16_t* S, const uint16_t* X, uin
   return launch_status();
 }
 
-// Tile-shape override for measurement (CUDALM_W4A16_GEMM_CFG); -1 = by shape.
-int gemm_config() {
-  static const int cfg = env_setting("CUDALM_W4A16_GEMM_CFG", -1, -1, 99);
-  return cfg;
-}
-
+// Prefill chunks (M >= 33). The 32 x 32 MFMA GEMM (w4a16_gemm.hip: 32
+// activation rows x 256 weight rows per 8-wave workgroup) serves K <= 1024
+// when its workgroups fill between 3/4 and all of the CUs in one round
+// (3584x1024 and 4096x1024 at M = 512: 10.3 -> 9.6-9.9 us, 10.7 -> 9.5-10.0 us);
+// elsewhere the 16 x 16 unit GEMM is faster (one round of 32 x 256 tiles
+// leaves too many CUs idle below that, and past one round it takes two).
+// Unit GEMM tiles: 128 x 32 of 8 waves while they fill most of the CUs,
+// else 64 x 32 of 4 waves, with two k-slices of 4 waves when K spans
+// several units (1024x3584 at M = 512: 16.7 -> 14.6 us). The 4-wave tiles
+// run their offset chains inline (512x1024x512 5.8 -> 5.5 us, 1024x3584x512
+// 14.4 -> 13.8 us); inline chains cost the 8-wave tiles 0.6 us at
+// 3584x1024x512, so those keep the table.
 template <bool PACKED>
 int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N, int K,
                    int M, hipStream_t stream) {
-  int cfg = gemm_config();
-  if (cfg < 0 || cfg >= 40) {
-    const int rc = launch_prefill_group<PACKED>(W, S, X, Y, N, K, M, cfg, stream);
-    if (rc != 1) return rc;
-    cfg = 1;
+  const int cus = cu_count();
+  if (K <= kUnit * kGroup) {
+    const long long wgs32 = static_cast<long long>((N + 255) / 256) * ((M + 31) / 32);
+    if (4 * wgs32 >= 3LL * cus && wgs32 <= cus)
+      return launch_prefill32<PACKED>(W, S, X, Y, N, K, M, stream);
   }
-  if (cfg == 1) {
-    // unit GEMM: 128 x 32 workgroup tiles of 8 waves while they fill most
-    // of the CUs, else 64 x 32 tiles of 4 waves, with two k-slices of 4 waves when
-    // K spans several units (1024x3584 at M = 512: 16.7 -> 14.6 us). The
-    // 4-wave tiles run their offset chains inline (512x1024x512 5.8 ->
-    // 5.5 us, 1024x3584x512 14.4 -> 13.8 us); inline chains cost the
-    // 8-wave tiles 0.6 us at 3584x1024x512, so those keep the table.
-    const long long wgs = static_cast<long long>((N + 127) / 128) * ((M + 31) / 32);
-    // (crossover measured between 128 and 168 workgroups of 128 x 32:
-    // 2048x1024x256 5.7 vs 6.9 us, 3584x1024x192 7.4 vs 6.9 us)
-    cfg = 5 * wgs >= 3LL * cu_count() ? 24 : (K > kUnit * kGroup ? 30 : 25);
-  }
-  switch (cfg) {
-    // measurement alternatives: the tile kernel (9), other unit-GEMM tile
-    // shapes (21-23); 30 is the two-k-slice unit GEMM
-    case 9: return launch_tile<2, 4, 2, 2, 2, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 21: return launch_gemm_unit<1, 4, 8, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 22: return launch_gemm_unit<1, 4, 4, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 23: return launch_gemm_unit<2, 2, 4, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 24: return launch_gemm_unit<1, 2, 8, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 27: return launch_gemm_unit<2, 4, 4, PACKED>(W, S, X, Y, N, K, M, stream);
-    case 30: return launch_gemm_unit<1, 2, 4, PACKED, 2, true>(W, S, X, Y, N, K, M, stream);
-    default: return launch_gemm_unit<1, 2, 4, PACKED, 1, true>(W, S, X, Y, N, K, M, stream);
-  }
+  const long long wgs = static_cast<long long>((N + 127) / 128) * ((M + 31) / 32);
+  // (crossover measured between 128 and 168 workgroups of 128 x 32:
+  // 2048x1024x256 5.7 vs 6.9 us, 3584x1024x192 7.4 vs 6.9 us)
+  if (5 * wgs >= 3LL * cus) return launch_gemm_unit<1, 2, 8, PACKED>(W, S, X, Y, N, K, M, stream);
+  if (K > kUnit * kGroup)
+    return launch_gemm_unit<1, 2, 4, PACKED, 2, true>(W, S, X, Y, N, K, M, stream);
+  return launch_gemm_unit<1, 2, 4, PACKED, 1, true>(W, S, X, Y, N, K, M, stream);
 }
 
 template <class Act = ActBf16>
@@ -2287,6 +2111,8 @@ int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y
       return launch_tile<1, 2, 4, 1, 8, PACKED>(W, S, X, Y, N, K, M, stream);
     case CUDALM_W4A16_VARIANT_PREFILL:
       return launch_prefill<PACKED>(W, S, X, Y, N, K, M, stream);
+    case CUDALM_W4A16_VARIANT_PREFILL32:
+      return launch_prefill32<PACKED>(W, S, X, Y, N, K, M, stream);
     case CUDALM_W4A16_VARIANT_BYTEWISE:
       if (PACKED) return CUDALM_W4A16_EVARIANT;
       return launch_bytewise(W, S, X, Y, N, K, M, stream);
@@ -2316,11 +2142,6 @@ int f16_dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_
 
 }  // namespace
 
-#ifdef CUDALM_SPLIT_PROBE
-extern "C" int cudalm_split_probe_read(void* host, size_t bytes) {
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_split_probe), bytes) == hipSuccess ? 0 : -1;
-}
-#endif
 
 extern "C" {
 
@@ -2527,7 +2348,8 @@ int cudalm_w4a16_kernel_regs(int variant) {
       return regs_of(w4a16_stream_piece_kernel<true, 1, false, 1, ActBf16, 4, true>);
     case CUDALM_W4A16_VARIANT_TILE16: return regs_of(w4a16_tile_kernel<1, 1, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_TILE32: return regs_of(w4a16_tile_kernel<1, 2, 4, 1, 8, true>);
-    case CUDALM_W4A16_VARIANT_PREFILL: return prefill_group_regs();
+    case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_gemm_unit_kernel<1, 2, 8, true, false>);
+    case CUDALM_W4A16_VARIANT_PREFILL32: return prefill32_regs();
     case CUDALM_W4A16_VARIANT_BYTEWISE: return regs_of(w4a16_bytewise_kernel<ActBf16>);
     case CUDALM_W4A16_VARIANT_SPLIT: return regs_of(w4a16_split_kernel<true, 1, false, 1>);
     case CUDALM_W4A16_VARIANT_SWIGLU: return regs_of(w4a16_swiglu_kernel<true, 1, false, 1>);

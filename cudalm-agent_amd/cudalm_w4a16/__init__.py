@@ -103,6 +103,7 @@ VARIANT_PREFILL = 4
 VARIANT_BYTEWISE = 5
 VARIANT_SPLIT = 6
 VARIANT_SWIGLU = 7  # kernel_regs only
+VARIANT_PREFILL32 = 8
 VARIANTS = {
     "split": VARIANT_SPLIT,
     "auto": VARIANT_AUTO,
@@ -110,6 +111,7 @@ VARIANTS = {
     "tile16": VARIANT_TILE16,
     "tile32": VARIANT_TILE32,
     "prefill": VARIANT_PREFILL,
+    "prefill32": VARIANT_PREFILL32,
     "bytewise": VARIANT_BYTEWISE,
 }
 

@@ -235,10 +235,11 @@ int cudalm_w4a16_dequant_f32(const uint8_t* weight, const uint16_t* scale,
 #define CUDALM_W4A16_VARIANT_STREAM 1   /* M <= 32, x resident in LDS */
 #define CUDALM_W4A16_VARIANT_TILE16 2   /* 16 columns per wave, K chunked */
 #define CUDALM_W4A16_VARIANT_TILE32 3   /* 32 columns per wave, K chunked */
-#define CUDALM_W4A16_VARIANT_PREFILL 4  /* 64x64 per wave, 128x128 per group */
+#define CUDALM_W4A16_VARIANT_PREFILL 4  /* prefill GEMM chosen by shape (M >= 33) */
 #define CUDALM_W4A16_VARIANT_BYTEWISE 5 /* misaligned-base fallback */
 #define CUDALM_W4A16_VARIANT_SPLIT 6    /* M <= 32, units of a tile on separate waves */
 #define CUDALM_W4A16_VARIANT_SWIGLU 7   /* kernel_regs only: the fused SwiGLU kernel */
+#define CUDALM_W4A16_VARIANT_PREFILL32 8 /* 32x32 MFMA GEMM, 32 x 256 per workgroup */
 int cudalm_w4a16_gemv_bf16_variant(const uint8_t* weight, const uint16_t* scale,
                                    const uint16_t* x, uint16_t* y, int N, int K,
                                    int M, int variant, hipStream_t stream);

@@ -1,0 +1,48 @@
+"""The 32 x 32 MFMA prefill GEMM (w4a16_gemm.hip), forced with
+CUDALM_W4A16_VARIANT_PREFILL32 on census shapes and ragged ones (N not a
+multiple of 32 or of 256, M not a multiple of 32, a short last 8-group
+unit, K spanning several units, file-layout scale rows not 16 B aligned),
+both weight layouts. Outputs must equal the tile kernel's bit for bit (the
+per-output operation sequence every kernel shares: each 16 x 16 x 32 MFMA
+step equals two 32 x 32 x 16 steps over its k-block halves) and be within
+the oracle's bound (the restatement of tests/cuda/test_int4_gemv_bf16.cpp:
+54-69). Every row equals the single-row call on it."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    torch.cuda.synchronize()
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("N,K,M", [(3584, 1024, 512), (4096, 1024, 512), (1000, 1024, 70),
+                                   (16, 1024, 33), (2048, 1024, 129), (1024, 3584, 100),
+                                   (1024, 2048, 64), (37, 384, 40), (300, 2176, 97),
+                                   (1, 128, 33), (257, 1024, 1)])
+def test_prefill32_bit_identity(w4, orc, dev, N, K, M):
+    W, S = orc.synth_w4a16(0x919E + N + M + K, N, K)
+    X = orc.synth_act(0x919F + M, M, K)
+    w = torch.from_numpy(W).to(dev)
+    s = torch.from_numpy(S.view(np.int16)).to(dev).view(torch.float16)
+    x = torch.from_numpy(X.view(np.int16)).to(dev).view(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    w4.gemv(w, s, x, N, K, M, y=y, variant="prefill32")
+    yt = torch.empty_like(y)
+    w4.gemv(w, s, x, N, K, M, y=yt, variant="tile32")
+    p = w4.repack(w, s, N, K)
+    yp = torch.empty_like(y)
+    w4.gemv_prepacked(p, x, N, K, M, y=yp, variant="prefill32")
+    Y = _bits(y).reshape(M, N)
+    assert np.array_equal(Y, _bits(yt).reshape(M, N)), ("tile32", N, K, M)
+    assert np.array_equal(Y, _bits(yp).reshape(M, N)), ("prepacked", N, K, M)
+    ok, st = orc.check_tolerance(Y, W, S, X, N, K, M)
+    print(f"  prefill32 N={N} K={K} M={M}: {st}", flush=True)
+    assert ok, st
+    for b in sorted({0, M // 2, M - 1}):
+        y1 = torch.empty((1, N), dtype=torch.bfloat16, device=dev)
+        w4.gemv(w, s, x[b:b + 1], N, K, 1, y=y1)
+        assert np.array_equal(Y[b], _bits(y1).reshape(N)), b
