@@ -367,9 +367,15 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
 #pragma unroll
           for (int r = 0; r < NR; ++r) {
             const int m = ct * 16 + 4 * a + r;
-            if (m < M)
+            if (m < M) {
+              // a NaN sum (infinite or NaN activations, overflow) is
+              // recomputed by the reference loop, keeping its semantics
+              float val = 16.0f * total[ct][r];
+              if (__builtin_expect(val != val, 0))
+                val = w4a16_ref_dot<PACKED, false, true>(v.w, v.s, K, n, S.x + static_cast<size_t>(m) * K);
               st_dev_u16(col + static_cast<size_t>(m) * Nj,
-                         static_cast<uint16_t>(f32_to_bf16_rne(16.0f * total[ct][r])));
+                         static_cast<uint16_t>(f32_to_bf16_rne(val)));
+            }
           }
       }
       __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete

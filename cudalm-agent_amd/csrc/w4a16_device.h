@@ -80,6 +80,52 @@ __device__ __forceinline__ f32x4_t group_offset(const u32x4_t (&xa)[4]) {
   return c;
 }
 
+// The reference's own loop for one output (tests/cuda/test_int4_gemv_bf16.cpp:
+// 54-69; the fp16 twin, tests/cuda/test_int4_gemv.cpp:49-63): fp32, k
+// ascending, each term (q * f32(s)) * f32(x). The kernels call it only for
+// an output whose fast sum is NaN. That sum cancels the decode's 1.5 bias
+// with a second chain over -1.5 * x, so an infinite activation turns into
+// Inf - Inf there, where the reference gives +-Inf when every infinite term
+// has one sign (and NaN otherwise, or for a NaN activation, or a zero weight
+// or scale times an infinity); overflowing finite sums are the same case.
+// Recomputing those outputs in the reference's order gives the reference's
+// result. W is the projection's weights (file layout [N, K/2], or prepacked:
+// tile-major, dwords rotated left by 3), S its fp16 scales (file layout
+// only), xrow the activation row (bf16, or fp16 when F16), read with
+// device-coherent loads when XCOH (x written by another workgroup of the
+// same launch).
+template <bool PACKED, bool F16 = false, bool XCOH = false>
+__device__ __forceinline__ float w4a16_ref_dot(const uint8_t* W, const uint16_t* S, int K, int n,
+                                            const uint16_t* xrow) {
+  const int G = K >> 7;
+  const uint8_t* tile = W + static_cast<size_t>(n >> 4) * packed_tile_bytes(G);
+  const int i = n & 15;
+  float acc = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const int g = k >> 7;
+    int nib;
+    float s;
+    if constexpr (PACKED) {
+      const int kk = k & 127;
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(
+          tile + static_cast<size_t>(g) * 1024 + 16 * (16 * (kk >> 5) + i) + 4 * ((kk >> 3) & 3));
+      nib = static_cast<int>((rotr(w, 3) >> (4 * (kk & 7))) & 15u);
+      s = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(
+          tile + static_cast<size_t>(G) * 1024 + i * packed_scale_pitch(G) + 2 * g));
+    } else {
+      const uint8_t b = W[static_cast<size_t>(n) * (K >> 1) + (k >> 1)];
+      nib = (k & 1) ? (b >> 4) : (b & 15);
+      s = half_bits_to_f32(S[static_cast<size_t>(n) * G + g]);
+    }
+    const float q = static_cast<float>((nib ^ 8) - 8);
+    const uint32_t xb =
+        XCOH ? __hip_atomic_load(xrow + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : xrow[k];
+    const float x = F16 ? half_bits_to_f32(xb) : bf16_lo(xb);
+    acc += (q * s) * x;
+  }
+  return acc;
+}
+
 // Prefill-chunk GEMM on 32 x 32 MFMA tiles (w4a16_gemm.hip): 32 activation
 // rows x 256 weight rows per 8-wave workgroup, any M, N and K % 128 == 0.
 template <bool PACKED>

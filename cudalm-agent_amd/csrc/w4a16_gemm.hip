@@ -267,9 +267,14 @@ __global__ __launch_bounds__(WVN * 64) void w4a16_gemm32_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (m < mrows)
-          Y[static_cast<size_t>(m0 + m) * N + n] =
-              static_cast<uint16_t>(f32_to_bf16_rne(16.0f * acc[nb][mt][r]));
+        if (m < mrows) {
+          // a NaN sum (infinite or NaN activations, overflow) is recomputed
+          // by the reference loop, which keeps the reference's semantics
+          float v = 16.0f * acc[nb][mt][r];
+          if (__builtin_expect(v != v, 0))
+            v = w4a16_ref_dot<PACKED>(W, S, K, n, X + static_cast<size_t>(m0 + m) * K);
+          Y[static_cast<size_t>(m0 + m) * N + n] = static_cast<uint16_t>(f32_to_bf16_rne(v));
+        }
       }
   }
 }

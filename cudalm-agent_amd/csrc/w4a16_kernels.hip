@@ -432,9 +432,69 @@ __device__ __forceinline__ void stream_unit(f32x4_t (&part)[CT], const StreamUni
   }
 }
 
-template <int NR, int CT, class Act = ActBf16, class PT = ProjTable>
+// The output of one accumulator: kUnit * total, or, when that is NaN, the
+// reference loop's sum for the output (w4a16_ref_dot: infinite and NaN
+// activations and overflow keep the reference's semantics).
+template <class Act, bool PACKED>
+__device__ __forceinline__ float out_value(float total, const uint8_t* w, const uint16_t* s, int K,
+                                           int n, const uint16_t* xrow) {
+  const float v = Act::kUnit * total;
+  if (__builtin_expect(v != v, 0))
+    return w4a16_ref_dot<PACKED, std::is_same<Act, ActF16>::value>(w, s, K, n, xrow);
+  return v;
+}
+
+// Deferred form (the pair kernel, whose pipelined loop holds two tiles'
+// accumulators): the fast values are stored and NaNs reported; the kernel
+// re-walks its tiles with fix_tile after its loop when any lane saw one, so
+// the reference loop adds no registers to the loop.
+template <int NR, int CT, class Act, class PT>
+__device__ __forceinline__ bool store_tile_fast(const PT& P, int t, const f32x4_t (&total)[CT],
+                                                int M, int i, int a) {
+  const ProjView v = proj_view(P, t);
+  const int Nj = v.n;
+  const int n = (t - v.begin) * kTileRows + i;
+  if (n >= Nj) return false;
+  uint16_t* col = v.y + static_cast<size_t>(4 * a) * Nj + n;
+  bool nan = false;
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (ct * 16 + 4 * a + r < M) {
+        const float f = Act::kUnit * total[ct][r];
+        nan = nan || f != f;
+        col[static_cast<size_t>(ct * 16 + r) * Nj] = static_cast<uint16_t>(Act::round(f));
+      }
+    }
+  return nan;
+}
+
+// Recompute the NaN outputs of tile t (written by store_tile_fast) with the
+// reference loop.
+template <int NR, int CT, class Act, class PT, bool PACKED>
+__device__ __forceinline__ void fix_tile(const PT& P, int t, int M, int i, int a, const uint16_t* X,
+                                      int K) {
+  const ProjView v = proj_view(P, t);
+  const int Nj = v.n;
+  const int n = (t - v.begin) * kTileRows + i;
+  if (n >= Nj) return;
+  uint16_t* col = v.y + static_cast<size_t>(4 * a) * Nj + n;
+  for (int ct = 0; ct < CT; ++ct)
+    for (int r = 0; r < NR; ++r) {
+      const int m = ct * 16 + 4 * a + r;
+      if (m >= M) continue;
+      uint16_t* yp = col + static_cast<size_t>(ct * 16 + r) * Nj;
+      if ((*yp & 0x7FFFu) > 0x7F80u || (Act::kUnit == 16.0f && std::is_same<Act, ActF16>::value &&
+                                         (*yp & 0x7FFFu) > 0x7C00u))
+        *yp = static_cast<uint16_t>(Act::round(w4a16_ref_dot<PACKED, std::is_same<Act, ActF16>::value>(
+            v.w, v.s, K, n, X + static_cast<size_t>(m) * K)));
+    }
+}
+
+template <int NR, int CT, class Act, class PT, bool PACKED>
 __device__ __forceinline__ void store_tile(const PT& P, int t, const f32x4_t (&total)[CT],
-                                           int M, int i, int a) {
+                                           int M, int i, int a, const uint16_t* X, int K) {
   const ProjView v = proj_view(P, t);
   const int Nj = v.n;
   const int n = (t - v.begin) * kTileRows + i;
@@ -445,9 +505,10 @@ __device__ __forceinline__ void store_tile(const PT& P, int t, const f32x4_t (&t
   for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      if (ct * 16 + 4 * a + r < M)
-        col[static_cast<size_t>(ct * 16 + r) * Nj] =
-            static_cast<uint16_t>(Act::round(Act::kUnit * total[ct][r]));
+      const int m = ct * 16 + 4 * a + r;
+      if (m < M)
+        col[static_cast<size_t>(ct * 16 + r) * Nj] = static_cast<uint16_t>(Act::round(
+            out_value<Act, PACKED>(total[ct][r], v.w, v.s, K, n, X + static_cast<size_t>(m) * K)));
     }
 }
 
@@ -614,10 +675,12 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
   // then stores the tile finished in the previous step, then issues the
   // next piece's loads, so no wait ever covers a store issued just before
   // it. The two piece buffers alternate (two steps per loop turn).
+  const int t_first = t;
+  bool nan_seen = false;
   auto step = [&](const StreamPiece<HG>& cur, StreamPiece<HG>& nxt) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt at their maxima
     if (done_t >= 0) {
-      store_tile<NR, CT, Act, PT>(P, done_t, done, M, i, a);
+      nan_seen |= store_tile_fast<NR, CT, Act, PT>(P, done_t, done, M, i, a);
       done_t = -1;
     }
     int nt = t, nh = h + 1;
@@ -658,7 +721,14 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
   };
   while (step(bufA, bufB) && step(bufB, bufA)) {
   }
-  if (done_t >= 0) store_tile<NR, CT, Act, PT>(P, done_t, done, M, i, a);
+  if (done_t >= 0) nan_seen |= store_tile_fast<NR, CT, Act, PT>(P, done_t, done, M, i, a);
+  if (__builtin_expect(__builtin_amdgcn_ballot_w64(nan_seen) != 0, 0)) {
+    // a NaN sum (infinite or NaN activations, overflow): those outputs are
+    // recomputed by the reference loop, which keeps its semantics
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
+    for (int tt = t_first; tt < ntiles; tt += stride)
+      fix_tile<NR, CT, Act, PT, PACKED>(P, tt, M, i, a, X, K);
+  }
 }
 
 // Split kernel: few weight tiles, several units per tile (K >= 2048). A
@@ -709,6 +779,8 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_kernel(
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) part[k][ct] = total[k][ct] = zero;
   int h = 0;
+  const int p_first = p;
+  bool nan_seen = false;
   while (true) {
     int np = p, nh = h + 1;
     if (nh == H) {
@@ -758,7 +830,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_kernel(
     if (h == H - 1) {
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        if (2 * p + k < ntiles) store_tile<NR, CT, Act, PT>(P, 2 * p + k, total[k], M, i, a);
+        if (2 * p + k < ntiles) nan_seen |= store_tile_fast<NR, CT, Act, PT>(P, 2 * p + k, total[k], M, i, a);
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) total[k][ct] = zero;
       }
@@ -771,6 +843,14 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_kernel(
     }
     p = np;
     h = nh;
+  }
+  if (__builtin_expect(__builtin_amdgcn_ballot_w64(nan_seen) != 0, 0)) {
+    // a NaN sum (infinite or NaN activations, overflow): those outputs are
+    // recomputed by the reference loop, which keeps its semantics
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
+    for (int pp = p_first; pp < npairs; pp += stride)
+      for (int k = 0; k < 2; ++k)
+        if (2 * pp + k < ntiles) fix_tile<NR, CT, Act, PT, PACKED>(P, 2 * pp + k, M, i, a, X, K);
   }
 }
 
@@ -824,7 +904,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
       total[ct] = zero;
       for (int u = 0; u < U; ++u) total[ct] = total[ct] + slots[((wave * U + u) * CT + ct) * 64 + lane];
     }
-    store_tile<NR, CT, Act, PT>(P, t0 + wave, total, M, i, a);
+    store_tile<NR, CT, Act, PT, PACKED>(P, t0 + wave, total, M, i, a, X, K);
   }
 }
 
@@ -933,8 +1013,11 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
       for (int r = 0; r < NR; ++r) {
         const int m = ct * 16 + 4 * a + r;
         if (m < mrows && n < N)
-          P.y[0][static_cast<size_t>(m0 + m) * N + n] = static_cast<uint16_t>(
-              silu_mul_bits(f32_to_bf16_rne(16.0f * tg[r]), f32_to_bf16_rne(16.0f * tu[r])));
+          P.y[0][static_cast<size_t>(m0 + m) * N + n] = static_cast<uint16_t>(silu_mul_bits(
+              f32_to_bf16_rne(out_value<ActBf16, PACKED>(tg[r], P.w[0], P.s[0], K, n,
+                                                         X + static_cast<size_t>(m0 + m) * K)),
+              f32_to_bf16_rne(out_value<ActBf16, PACKED>(tu[r], P.w[1], P.s[1], K, n,
+                                                         X + static_cast<size_t>(m0 + m) * K))));
       }
     }
   }
@@ -1093,7 +1176,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
       }
     }
     if constexpr (NP == 1) {
-      store_tile<NR, CT, Act, PT>(P, t0 + wave, total[0], M, i, a);
+      store_tile<NR, CT, Act, PT, PACKED>(P, t0 + wave, total[0], M, i, a, X, K);
     } else {
       const int N = P.n[0];
       const int n = (t0 + wave) * kTileRows + i;
@@ -1103,9 +1186,12 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
         for (int r = 0; r < NR; ++r) {
           const int m = ct * 16 + 4 * a + r;
           if (m < mrows && n < N)
-            P.y[0][static_cast<size_t>(m0 + m) * N + n] = static_cast<uint16_t>(
-                silu_mul_bits(f32_to_bf16_rne(16.0f * total[0][ct][r]),
-                              f32_to_bf16_rne(16.0f * total[NP - 1][ct][r])));
+            P.y[0][static_cast<size_t>(m0 + m) * N + n] = static_cast<uint16_t>(silu_mul_bits(
+                f32_to_bf16_rne(out_value<ActBf16, PACKED>(total[0][ct][r], P.w[0], P.s[0], K, n,
+                                                           Xc + static_cast<size_t>(m) * K)),
+                f32_to_bf16_rne(out_value<ActBf16, PACKED>(total[NP - 1][ct][r], P.w[NP - 1],
+                                                           P.s[NP - 1], K, n,
+                                                           Xc + static_cast<size_t>(m) * K))));
         }
     }
   }
@@ -1235,8 +1321,9 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
       for (int r = 0; r < 4; ++r) {
         const int ml = wm * CT * 16 + ct * 16 + 4 * a + r;
         if (ml < mrows)
-          Y[static_cast<size_t>(m0 + ml) * N + n] =
-              static_cast<uint16_t>(f32_to_bf16_rne(16.0f * total[rb][ct][r]));
+          Y[static_cast<size_t>(m0 + ml) * N + n] = static_cast<uint16_t>(
+              f32_to_bf16_rne(out_value<ActBf16, PACKED>(total[rb][ct][r], W, S, K, n,
+                                                         X + static_cast<size_t>(m0 + ml) * K)));
       }
   }
 }
@@ -1487,8 +1574,9 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         if (ct * 16 + 4 * a + r < mrows)
-          col[static_cast<size_t>(ct * 16 + r) * N] =
-              static_cast<uint16_t>(f32_to_bf16_rne(16.0f * total[rb][ct][r]));
+          col[static_cast<size_t>(ct * 16 + r) * N] = static_cast<uint16_t>(f32_to_bf16_rne(
+              out_value<ActBf16, PACKED>(total[rb][ct][r], W, S, K, n,
+                                         X + static_cast<size_t>(m0 + ct * 16 + 4 * a + r) * K)));
   }
 }
 

@@ -191,3 +191,26 @@ def test_chain_one_shot_and_errors(orc, w4, dev):
     st[1].K = K
     st[1].x = x.data_ptr() + 2
     assert bad(2, M, nbytes) == w4.EALIGN
+
+
+def test_chain_infinite_activation(orc, w4, dev):
+    """An infinity in x: each chain output equals cudalm_w4a16_gemv_bf16's,
+    which gives the reference loop's +-Inf / NaN there."""
+    N, K, M = 1024, 1024, 4
+    W, S = orc.synth_w4a16(0xC4A1E000, N, K)
+    X = orc.synth_act(0xC4A1E001, M, K)
+    X[2, 17] = 0xFF80  # -Inf
+    w = torch.from_numpy(W).to(dev)
+    s = torch.from_numpy(S.view(np.int16)).to(dev).view(torch.float16)
+    x = torch.from_numpy(X.view(np.int16)).to(dev).view(torch.bfloat16)
+    p = w4.repack(w, s, N, K)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    chain = w4.Chain([([(p.data_ptr(), None, y.data_ptr(), N)], x, K, -1)], M, prepacked=True)
+    chain.run()
+    chain.status()
+    ref = torch.empty_like(y)
+    w4.gemv_prepacked(p, x, N, K, M, y=ref)
+    assert np.array_equal(_bits(y), _bits(ref))
+    r = orc.gemv_bf16(W, S, X, N, K, M)
+    assert np.array_equal(np.isinf(orc.bf16_to_f32(_bits(y).reshape(M, N)[2])),
+                          np.isinf(orc.bf16_to_f32(r[2])))

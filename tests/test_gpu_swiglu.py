@@ -114,6 +114,34 @@ def test_fused_swiglu_equals_three_step(w4, orc, dev, N, K, M, packed):
     assert d.max() <= 1 and (d != 0).sum() <= max(1, d.size // 1000)
 
 
+@pytest.mark.parametrize("M", [1, 8, 33])
+@pytest.mark.parametrize("packed", [False, True])
+def test_fused_swiglu_infinite_activation(w4, orc, dev, M, packed):
+    """A row of x with an infinity: the fused launch still equals the
+    three-step sequence, whose projections give the reference loop's +-Inf /
+    NaN outputs (ref_gemv_bf16, tests/cuda/test_int4_gemv_bf16.cpp:54-69)."""
+    N, K = 3584, 1024
+    Wg, Sg = orc.synth_w4a16(0x1F6A, N, K)
+    Wu, Su = orc.synth_w4a16(0x1F6B, N, K)
+    X = orc.synth_act(0x1F6C + M, M, K)
+    X[M - 1, 300] = 0x7F80  # +Inf
+    gw = torch.from_numpy(Wg).to(dev)
+    uw = torch.from_numpy(Wu).to(dev)
+    gs, us, x = up(dev, Sg, Su, X)
+    gs, us, x = gs.view(torch.float16), us.view(torch.float16), x.view(torch.bfloat16)
+    if packed:
+        gw, uw = w4.repack(gw, gs, N, K), w4.repack(uw, us, N, K)
+    g, u, y3 = three_step(w4, gw, gs, uw, us, x, N, K, M, packed)
+    ref_g = orc.gemv_bf16(Wg, Sg, X, N, K, M)
+    gi = g.reshape(M, N)[M - 1]
+    assert np.array_equal(np.isinf(orc.bf16_to_f32(gi)), np.isinf(orc.bf16_to_f32(ref_g[M - 1])))
+    assert np.isinf(orc.bf16_to_f32(gi)).sum() > N // 2
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    w4.swiglu(gw, None if packed else gs, uw, None if packed else us, x, N, K, M, y=y,
+              prepacked=packed)
+    assert np.array_equal(down(y).reshape(M, N), y3.reshape(M, N))
+
+
 def test_fused_swiglu_rejects_bad_input(w4, dev):
     x = torch.zeros((1, 1024), dtype=torch.bfloat16, device=dev)
     w = torch.zeros(512 * 512, dtype=torch.uint8, device=dev)

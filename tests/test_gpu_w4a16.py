@@ -248,23 +248,55 @@ def test_lm_head_full_size(w4, orc, dev):
     assert np.array_equal(orc.bf16_to_f32(Y2), orc.bf16_to_f32(Y) * 2)
 
 
-@pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
-def test_nonfinite_activation(w4, orc, dev, bad):
-    # every output sums over every k, so one non-finite x[k] makes every
-    # output of that row non-finite in the reference (ref_gemv_bf16 gives
-    # +-Inf or NaN); the 1.5 offset cancellation gives NaN for an infinity.
-    # Other batch rows are untouched (row independence).
-    N, K, M = 512, 1024, 3
+def _same_nonfinite(a, b):
+    """bit-equal, NaN payloads aside (any NaN equals any NaN)"""
+    fa, fb = np.asarray(a, np.uint16), np.asarray(b, np.uint16)
+    na = ((fa & 0x7F80) == 0x7F80) & ((fa & 0x7F) != 0)
+    nb = ((fb & 0x7F80) == 0x7F80) & ((fb & 0x7F) != 0)
+    return np.array_equal(na, nb) and np.array_equal(fa[~na], fb[~nb])
+
+
+@pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan, "mixed"])
+@pytest.mark.parametrize("M", [3, 40])
+def test_nonfinite_activation(w4, orc, dev, bad, M):
+    # Rows of x holding a non-finite value give the reference loop's outputs
+    # (ref_gemv_bf16, tests/cuda/test_int4_gemv_bf16.cpp:54-69): +-Inf where
+    # every infinite term has one sign, NaN where a term is NaN (a NaN x, a
+    # zero weight or scale times an infinity, or +Inf and -Inf terms). The
+    # kernels recompute an output whose fast sum is NaN with that loop, so
+    # the rows equal the oracle's (NaN payloads aside); other rows are
+    # untouched (row independence). Every kernel family, both layouts.
+    N, K = 512, 1024
     W, S, X = orc.fixture_kind("random", 0x51, N, K, M)
     Xb = X.copy()
-    Xb[1, 77] = orc.f32_to_bf16(np.array([bad], np.float32))[0]
-    w, s, x = up(dev, W, S, Xb)
-    for variant in ("auto", "stream", "tile16", "prefill"):
+    if bad == "mixed":
+        Xb[1, 77] = orc.f32_to_bf16(np.array([np.inf], np.float32))[0]
+        Xb[1, 900] = orc.f32_to_bf16(np.array([-np.inf], np.float32))[0]
+    else:
+        Xb[1, 77] = orc.f32_to_bf16(np.array([bad], np.float32))[0]
+    # a row whose only infinity meets no zero weight: every output +-Inf
+    Xb[M - 1, 5] = orc.f32_to_bf16(np.array([np.inf], np.float32))[0]
+    Wz = W.copy()
+    Wz[:, 2] = np.where((Wz[:, 2] & 0xF0) == 0, Wz[:, 2] | 0x10, Wz[:, 2])  # q[n, 5] != 0
+    ref = orc.gemv_bf16(Wz, S, Xb, N, K, M)
+    assert np.isinf(orc.bf16_to_f32(ref[M - 1])).all()
+    w, s, x = up(dev, Wz, S, Xb)
+    x0 = up(dev, Wz, S, X)[2]
+    p = w4.repack(w, s, N, K)
+    variants = ("auto", "stream", "split", "tile16", "tile32", "prefill", "prefill32", "bytewise")
+    for variant in variants:
+        if variant in ("stream", "split") and M > 32:
+            continue
         Y = run(w4, w, s, x, N, K, M, variant)
-        Yf = orc.bf16_to_f32(Y)
-        assert not np.isfinite(Yf[1]).any(), variant
-        Y0 = run(w4, *up(dev, W, S, X), N, K, M, variant)
-        assert np.array_equal(Y[[0, 2]], Y0[[0, 2]]), variant
+        for row in (1, M - 1):
+            assert _same_nonfinite(Y[row], ref[row]), (variant, row)
+        Y0 = run(w4, w, s, x0, N, K, M, variant)
+        keep = [r for r in range(M) if r not in (1, M - 1)]
+        assert np.array_equal(Y[keep], Y0[keep]), variant
+        if variant != "bytewise":
+            yp = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            w4.gemv_prepacked(p, x, N, K, M, y=yp, variant=variant)
+            assert np.array_equal(down(yp).reshape(M, N), Y), ("prepacked", variant)
 
 
 @pytest.mark.parametrize("N,M", [(248320, 8), (100003, 3), (100003, 1), (248320, 32)])
