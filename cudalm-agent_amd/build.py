@@ -112,7 +112,27 @@ def build_boundary_check(verbose: bool = False) -> str:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("hipcc failed building tests/cpp/boundary_check")
     os.replace(CHECK_BIN + ".tmp", CHECK_BIN)
+    build_round_check(verbose)
     return CHECK_BIN
+
+
+ROUND_SRC = os.path.join(REPO, "tests", "cpp", "bf16_round_check.hip")
+ROUND_BIN = os.path.join(REPO, "tests", "cpp", "bf16_round_check")
+
+
+def build_round_check(verbose: bool = False) -> str:
+    """tests/test_gpu_bf16_round.py's device program: the library's own
+    f32_to_bf16_rne (csrc/hip_common.h, same flags as the library)."""
+    cmd = [hipcc(), *[f for f in HIPCC_FLAGS if f != "-fPIC"], "-I", os.path.join(REPO, "include"),
+           "-I", CSRC, ROUND_SRC, "-o", ROUND_BIN + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed building tests/cpp/bf16_round_check")
+    os.replace(ROUND_BIN + ".tmp", ROUND_BIN)
+    return ROUND_BIN
 
 
 if __name__ == "__main__":

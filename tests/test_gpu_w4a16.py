@@ -59,14 +59,17 @@ THREADS = max(1, min(16, __import__("os").cpu_count() or 1))  # the GPU box's ho
 
 
 def assert_baseline(orc, Y, W, S, X, N, K, M, label=""):
-    """BASELINE workloads: every output within the bound; the count beyond
-    2 ulp is printed beside the reference CPU loop's on the same inputs.
-    (Per shape these are a handful of cancelled sums either way; the gate
-    that the kernels have no more of them than the loop is taken over whole
-    census traversals, tests/test_gpu_census.py.)"""
+    """BASELINE workloads: every output within the bound, and no more than 3
+    more outputs beyond 2 ulp than the reference CPU loop has on the same
+    inputs (a handful of cancelled sums either way; over whole census
+    traversals tests/test_gpu_census.py gates the totals with no slack)."""
     _, st, _ = orc.check_against_reference_loop(Y, W, S, X, N, K, M, THREADS)
     print(f"  {label} N={N} K={K} M={M}: {st}", flush=True)
     assert st["n_bad"] == 0, (label, st)
+    # outputs beyond 2 ulp are sums whose terms cancel: no more of them than
+    # the reference loop has on the same inputs, up to a few for the other
+    # accumulation order (either side can round one more of them badly)
+    assert st["n_over_2ulp"] <= st["ref_n_over_2ulp"] + 3, (label, st)
     return st
 
 
