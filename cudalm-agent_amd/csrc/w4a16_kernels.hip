@@ -132,9 +132,20 @@ __device__ __forceinline__ f32x4_t group_offset_t(const u32x4_t (&xa)[4]) {
   return c;
 }
 
+// LDS layout of staged activations. A row holds K/8 16-byte blocks plus
+// kXPad pad blocks, so rows start 2 blocks (mod 16) apart, and inside each
+// 128-column group the block of lane quarter a, step d (logical block
+// 4a + d, columns 32a + 8d ..) sits at slot 4d + a. One ds_read_b128 step
+// of a wave then reads 4 adjacent blocks from each of 16 rows: measured
+// conflict-free on gfx950 (4 LDS cycles per instruction), where unswizzled
+// rows 1 block (mod 16) apart spend half their cycles in bank conflicts.
+constexpr int kXPad = 2;
+__host__ __device__ constexpr int x_pitch(int kcl) { return (kcl >> 3) + kXPad; }
+__device__ __forceinline__ int x_slot(int c) { return (c & ~15) | ((c & 3) << 2) | ((c >> 2) & 3); }
+
 __device__ __forceinline__ void load_group_x(u32x4_t (&xa)[4], const u32x4_t* xgroup, int a) {
 #pragma unroll
-  for (int d = 0; d < 4; ++d) xa[d] = xgroup[4 * a + d];
+  for (int d = 0; d < 4; ++d) xa[d] = xgroup[4 * d + a];
 }
 
 // scale of group gg (0..7) from 8 packed fp16
@@ -155,6 +166,28 @@ struct StageBatch {
   u32x4_t v[kStageBatch];
 };
 
+// Row and block of the 16-byte blocks a thread stages: block e lies in row
+// e / nb at block e % nb, and a thread's blocks are `step` apart, so one
+// division per thread starts an incremental walk (step = dm rows + dc blocks)
+// instead of a division per block.
+struct StageWalk {
+  int mm, c, dm, dc, nb;
+  __device__ __forceinline__ StageWalk(int e0, int nb_, int step) : nb(nb_) {
+    mm = static_cast<int>(static_cast<unsigned>(e0) / static_cast<unsigned>(nb));
+    c = e0 - mm * nb;
+    dm = static_cast<int>(static_cast<unsigned>(step) / static_cast<unsigned>(nb));
+    dc = step - dm * nb;
+  }
+  __device__ __forceinline__ void next() {
+    c += dc;
+    mm += dm;
+    if (c >= nb) {
+      c -= nb;
+      ++mm;
+    }
+  }
+};
+
 // Batch b (blocks [b * 8 * blockDim.x, (b + 1) * 8 * blockDim.x)).
 __device__ __forceinline__ void stage_load(StageBatch& sb, const uint16_t* __restrict__ X, int K,
                                            int m0, int mrows, int k0, int kcl, int b) {
@@ -162,14 +195,17 @@ __device__ __forceinline__ void stage_load(StageBatch& sb, const uint16_t* __res
   const int total = mrows * nb;
   const int step = static_cast<int>(blockDim.x);
   const int first = b * kStageBatch * step;  // uniform
+  StageWalk wk(first + static_cast<int>(threadIdx.x), nb, step);
 #pragma unroll
   for (int q = 0; q < kStageBatch; ++q) {
     if (first + q * step < total) {  // uniform: whole batches of blocks
-      const int e = min(first + q * step + static_cast<int>(threadIdx.x), total - 1);
-      const int mm = e / nb;
-      sb.v[q] = *reinterpret_cast<const u32x4_t*>(X + static_cast<size_t>(m0 + mm) * K + k0 +
-                                                  8 * (e - mm * nb));
+      // blocks past the end re-read the last one
+      const bool in = first + q * step + static_cast<int>(threadIdx.x) < total;
+      const int mm = in ? wk.mm : mrows - 1;
+      const int c = in ? wk.c : nb - 1;
+      sb.v[q] = *reinterpret_cast<const u32x4_t*>(X + static_cast<size_t>(m0 + mm) * K + k0 + 8 * c);
     }
+    wk.next();
   }
 }
 
@@ -179,13 +215,11 @@ __device__ __forceinline__ void stage_store(u32x4_t* xs, int pitch, const StageB
   const int total = mrows * nb;
   const int step = static_cast<int>(blockDim.x);
   const int first = b * kStageBatch * step + static_cast<int>(threadIdx.x);
+  StageWalk wk(first, nb, step);
 #pragma unroll
   for (int q = 0; q < kStageBatch; ++q) {
-    const int e = first + q * step;
-    if (e < total) {
-      const int mm = e / nb;
-      xs[mm * pitch + (e - mm * nb)] = pair_order(sb.v[q]);
-    }
+    if (first + q * step < total) xs[wk.mm * pitch + x_slot(wk.c)] = pair_order(sb.v[q]);
+    wk.next();
   }
 }
 
@@ -521,7 +555,7 @@ __device__ __forceinline__ float* stream_prologue(u32x4_t* xs, const u32x4_t* (&
                                                   const uint16_t* __restrict__ X, int K, int M,
                                                   int wave, int i, int a, const StageBatch& sb0) {
   const int G = K >> 7;
-  const int pitch = (K >> 3) + 1;
+  const int pitch = x_pitch(K);
   float* corr = reinterpret_cast<float*>(xs + M * pitch);
   stage_store(xs, pitch, sb0, M, K, 0);
   stage_activations(xs, pitch, X, K, 0, M, 0, K, 1);
@@ -731,14 +765,9 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
   }
 }
 
-// Split kernel: few weight tiles, several units per tile (K >= 2048). A
-// workgroup takes TPR = max(1, 4/U) tiles; its waves compute the unit
-// partials of those tiles side by side, park them in LDS, and the unit
-// partials of each tile are summed in unit order. Same bits as the stream
-// kernel; shorter latency when tiles alone cannot fill the machine.
 // Pair stream kernel (single projection, two column tiles, M = 17..32):
 // as the piece stream kernel, but each wave streams two adjacent 16-row
-// weight tiles together, so every activation fragment and offset seed it
+// weight tiles together (three piece buffers, loads two pieces ahead), so every activation fragment and offset seed it
 // reads from LDS feeds the MFMAs of both tiles. At M = 32 the one-tile
 // kernel reads 64 KB of activation operands from LDS per weight tile, which
 // makes the LM head LDS-bound (~92 B/clk per CU) on top of its HBM stream;
@@ -761,13 +790,35 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_kernel(
 
   StageBatch sb0;
   stage_load(sb0, X, K, 0, M, 0, K, 0);
-  StreamPiece<HG> cur[2], nxt[2];
-  TileAddr acur[2];
+  // Three piece buffers: the loads run two pieces ahead of the compute, so
+  // two pieces (both tiles) are in flight while one is multiplied.
+  StreamPiece<HG> bufA[2], bufB[2], bufC[2];
+  const int p0 = min(p, npairs - 1);
+  TileAddr al[2];  // lane addresses of the pair being loaded
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    acur[k] = tile_addr<PACKED>(P, K, G, min(2 * min(p, npairs - 1) + k, ntiles - 1), lane);
-    stream_load_piece<HG, PACKED, SVEC, FULL>(cur[k], acur[k], G, 0);
-  }
+  for (int k = 0; k < 2; ++k) al[k] = tile_addr<PACKED>(P, K, G, min(2 * p0 + k, ntiles - 1), lane);
+  // load position: pair lp, piece lh (the first two pieces are issued here)
+  int lp = p, lh = 0;
+  auto load_next = [&](StreamPiece<HG>(&dst)[2]) {
+    const bool live = lp < npairs;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      TileAddr ad = al[k];
+      // past the last piece, load from the sink instead of branching around the loads
+      if (!live) ad.w = g_piece_sink + lane * 16;
+      stream_load_piece<HG, PACKED, SVEC, FULL>(dst[k], ad, G, (live ? lh : 0) * HG);
+    }
+    if (++lh == H) {
+      lh = 0;
+      lp += stride;
+      if (lp < npairs) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) al[k] = tile_addr<PACKED>(P, K, G, min(2 * lp + k, ntiles - 1), lane);
+      }
+    }
+  };
+  load_next(bufA);
+  load_next(bufB);
   const u32x4_t* xrow[CT];
   const float* corr = stream_prologue<CT, Act, false>(xs, xrow, X, K, M, wave, i, a, sb0);
   if (!active) return;
@@ -781,23 +832,12 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_kernel(
   int h = 0;
   const int p_first = p;
   bool nan_seen = false;
-  while (true) {
-    int np = p, nh = h + 1;
-    if (nh == H) {
-      nh = 0;
-      np = p + stride;
-    }
-    const bool has_next = np < npairs;
-    TileAddr anx[2] = {acur[0], acur[1]};
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      if (has_next && nh == 0) anx[k] = tile_addr<PACKED>(P, K, G, min(2 * np + k, ntiles - 1), lane);
-      // past the last piece, load from the sink instead of branching around the loads
-      if (!has_next) anx[k].w = g_piece_sink + lane * 16;
-      stream_load_piece<HG, PACKED, SVEC, FULL>(nxt[k], anx[k], G, (has_next ? nh : 0) * HG);
-    }
+  using L = Layout<Act, PACKED>;
+  // One piece of the current pair: issue the loads two pieces ahead into
+  // the buffer the previous step consumed, then multiply `cur`.
+  auto step = [&](const StreamPiece<HG>(&cur)[2], StreamPiece<HG>(&ld)[2]) {
+    load_next(ld);
     const int g0 = h * HG;
-    using L = Layout<Act, PACKED>;
 #pragma unroll
     for (int gg = 0; gg < HG; ++gg) {
       if (FULL || gg < G - g0) {
@@ -829,20 +869,20 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_kernel(
     }
     if (h == H - 1) {
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
+      for (int k = 0; k < 2; ++k)
         if (2 * p + k < ntiles) nan_seen |= store_tile_fast<NR, CT, Act, PT>(P, 2 * p + k, total[k], M, i, a);
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) total[k][ct] = zero;
-      }
-    }
-    if (!has_next) break;
+      for (int k = 0; k < 2; ++k)
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      cur[k] = nxt[k];
-      acur[k] = anx[k];
+        for (int ct = 0; ct < CT; ++ct) total[k][ct] = zero;
     }
-    p = np;
-    h = nh;
+    if (++h == H) {
+      h = 0;
+      p += stride;
+    }
+    return p < npairs;
+  };
+  while (step(bufA, bufC) && step(bufB, bufA) && step(bufC, bufB)) {
   }
   if (__builtin_expect(__builtin_amdgcn_ballot_w64(nan_seen) != 0, 0)) {
     // a NaN sum (infinite or NaN activations, overflow): those outputs are
@@ -854,12 +894,17 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_kernel(
   }
 }
 
+// Split kernel: few weight tiles, several units per tile (K >= 2048). A
+// workgroup takes TPR = max(1, 4/U) tiles; its waves compute the unit
+// partials of those tiles side by side, park them in LDS, and the unit
+// partials of each tile are summed in unit order. Same bits as the stream
+// kernel; shorter latency when tiles alone cannot fill the machine.
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, class PT = ProjTable>
 __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
     const PT P, const uint16_t* __restrict__ X, int K, int M) {
   extern __shared__ u32x4_t xs[];
   const int G = K >> 7;
-  const int pitch = (K >> 3) + 1;
+  const int pitch = x_pitch(K);
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   const int i = lane & 15, a = lane >> 4;
@@ -969,7 +1014,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
   const int t0 = blockIdx.x * TPR;
   const int m0 = blockIdx.y * mc;
   const int mrows = min(mc, M - m0);
-  const int pitch = (K >> 3) + 1;
+  const int pitch = x_pitch(K);
   f32x4_t* slots = reinterpret_cast<f32x4_t*>(
       reinterpret_cast<float*>(xs + mrows * pitch) + G * 16 * CT);
 
@@ -1041,7 +1086,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
   extern __shared__ u32x4_t xs[];
   constexpr int PPU = kUnit / HG;
   const int G = K >> 7;
-  const int pitch = (K >> 3) + 1;
+  const int pitch = x_pitch(K);
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   const int i = lane & 15, a = lane >> 4;
@@ -1210,7 +1255,7 @@ __global__ __launch_bounds__(WN * WM * 64) void w4a16_tile_kernel(
   extern __shared__ u32x4_t xs[];
   constexpr int CM = WM * CT * 16;
   constexpr int KC = GPC * kGroup;
-  constexpr int pitch = KC / 8 + 1;
+  constexpr int pitch = x_pitch(KC);
   const int G = K >> 7;
   const int ntiles = (N + kTileRows - 1) / kTileRows;
   const int lane = threadIdx.x & 63;
@@ -1353,7 +1398,7 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
     const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, int N, int K, int M) {
   constexpr int NT = WV * 64;  // threads of one k-slice
   constexpr int TM = CT * 16;
-  constexpr int PB = kUnit * 16 + 1;  // LDS row pitch in 16-byte blocks (padded)
+  constexpr int PB = x_pitch(kUnit * kGroup);  // LDS row pitch in 16-byte blocks (padded)
   constexpr int NBLK = TM * kUnit * 16;  // 16-byte x blocks per unit
   static_assert(NBLK % NT == 0, "staging must cover the tile exactly");
   constexpr int BPT = NBLK / NT;  // x blocks staged per thread per unit
@@ -1449,7 +1494,7 @@ __global__ __launch_bounds__(WV * KS * 64) void w4a16_gemm_unit_kernel(
     }
     if (it > 0) __syncthreads();  // previous unit's readers are done
     {
-      u32x4_t* xdst = xs + r0 * PB + b;
+      u32x4_t* xdst = xs + r0 * PB + x_slot(b);
 #pragma unroll
       for (int q = 0; q < BPT; ++q) xdst[q * RS * PB] = pair_order(v[q]);
     }
@@ -1717,7 +1762,7 @@ int check_shape(int N, int K, int M) {
 
 size_t stream_lds_bytes(int K, int M) {
   const int CT = M > 16 ? 2 : 1;
-  return static_cast<size_t>(M) * (K / 8 + 1) * 16 + static_cast<size_t>(K / kGroup) * 64 * CT;
+  return static_cast<size_t>(M) * x_pitch(K) * 16 + static_cast<size_t>(K / kGroup) * 64 * CT;
 }
 
 bool stream_fits(int K, int M) { return M <= 32 && stream_lds_bytes(K, M) <= kLdsMax; }
@@ -1836,7 +1881,7 @@ size_t split_piece_lds_bytes(int K, int M, SplitPlan p, int NP = 1) {
   const int U = (K / kGroup + kUnit - 1) / kUnit;
   const int ST = NP * U * PPU;
   const int tpr = ST >= p.wv ? 1 : p.wv / ST;
-  return (p.dx ? 0 : static_cast<size_t>(M) * (K / 8 + 1) * 16) +
+  return (p.dx ? 0 : static_cast<size_t>(M) * x_pitch(K) * 16) +
          static_cast<size_t>(tpr) * NP * U * CT * 64 * 16 * (1 + (PPU - 1) * p.hg) +
          static_cast<size_t>(tpr) * NP * U * (PPU - 1) * p.hg * 16 * 4;
 }
@@ -2075,7 +2120,7 @@ int launch_tile(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t
   constexpr int CM = WM * CT * 16;
   constexpr int KC = GPC * kGroup;
   const int mrows = M < CM ? M : CM;
-  const size_t lds = static_cast<size_t>(mrows) * (KC / 8 + 1) * 16;
+  const size_t lds = static_cast<size_t>(mrows) * x_pitch(KC) * 16;
   const int ntiles = (N + kTileRows - 1) / kTileRows;
   const int gx = (ntiles + WN * RB - 1) / (WN * RB);
   const int gy = (M + CM - 1) / CM;
@@ -2090,7 +2135,7 @@ template <int RB, int CT, int WV, bool PACKED, int KS = 1, bool IOFF = false>
 int launch_gemm_unit(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                      int K, int M, hipStream_t stream) {
   constexpr int TM = CT * 16;
-  const size_t xbytes = static_cast<size_t>(TM) * (kUnit * 16 + 1) * 16;
+  const size_t xbytes = static_cast<size_t>(TM) * x_pitch(kUnit * kGroup) * 16;
   const size_t lds = KS * (xbytes + static_cast<size_t>(kUnit) * CT * 16 * sizeof(float));
   const int G = K / kGroup;
   if constexpr (KS > 1) {

@@ -444,6 +444,31 @@ def test_piece_split_equals_stream(w4, orc, dev, N, K, M):
         assert np.array_equal(down(yp).reshape(M, N), Y), ("prepacked", name)
 
 
+@pytest.mark.parametrize("N,bad", [(100003, False), (100002, False), (40000, False), (100008, False),
+                                   (100008, True)])
+@pytest.mark.parametrize("M", [17, 24, 31, 32])
+def test_pair_kernel_edges(w4, orc, dev, N, bad, M):
+    # the pair kernel (one projection, M = 17..32, many tiles) against the
+    # tile kernel bit for bit: odd and even N, ragged last tiles and pairs,
+    # masked rows (M < 32), y at an odd element, an infinite activation (the
+    # reference loop's +-Inf / NaN outputs), and the element past y left
+    # untouched
+    K = 1024
+    W, S = orc.synth_w4a16(0x9A1 + N, N, K)
+    X = orc.synth_act(0x9A2 + M, M, K)
+    if bad:
+        X[M - 2, 77] = 0x7F80  # +Inf
+    w, s, x = up(dev, W, S, X)
+    ref = run(w4, w, s, x, N, K, M, "tile16")
+    p = w4.repack(w, s, N, K)
+    for shift in (0, 1):
+        buf = torch.full((M * N + 2,), float("nan"), dtype=torch.bfloat16, device=dev)
+        y = buf[shift:shift + M * N].view(M, N)
+        w4.gemv_prepacked(p, x, N, K, M, y=y, variant="stream")
+        assert np.array_equal(down(y).reshape(M, N), ref), ("shift", shift)
+        assert torch.isnan(buf[shift + M * N]).item(), ("guard", shift)
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_random_shapes_auto_equals_tile(w4, orc, dev, seed):
     # seeded random shapes across the dispatch plans (piece split of every
