@@ -478,10 +478,10 @@ __device__ __forceinline__ float out_value(float total, const uint8_t* w, const 
   return v;
 }
 
-// Deferred form (the pair kernel, whose pipelined loop holds two tiles'
-// accumulators): the fast values are stored and NaNs reported; the kernel
-// re-walks its tiles with fix_tile after its loop when any lane saw one, so
-// the reference loop adds no registers to the loop.
+// Deferred form (the streaming kernels' pipelined loops): the fast values
+// are stored and NaNs reported; the kernel re-walks its tiles with fix_tile
+// after its loop when any lane saw one, so the reference loop adds no
+// registers to the loop.
 template <int NR, int CT, class Act, class PT>
 __device__ __forceinline__ bool store_tile_fast(const PT& P, int t, const f32x4_t (&total)[CT],
                                                 int M, int i, int a) {
@@ -762,135 +762,6 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
     __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
     for (int tt = t_first; tt < ntiles; tt += stride)
       fix_tile<NR, CT, Act, PT, PACKED>(P, tt, M, i, a, X, K);
-  }
-}
-
-// Pair stream kernel (single projection, two column tiles, M = 17..32):
-// as the piece stream kernel, but each wave streams two adjacent 16-row
-// weight tiles together (three piece buffers, loads two pieces ahead), so every activation fragment and offset seed it
-// reads from LDS feeds the MFMAs of both tiles. At M = 32 the one-tile
-// kernel reads 64 KB of activation operands from LDS per weight tile, which
-// makes the LM head LDS-bound (~92 B/clk per CU) on top of its HBM stream;
-// pairs halve that. The per-output operation sequence is unchanged.
-template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, bool FULL, int WV, class PT>
-__global__ __launch_bounds__(WV * 64) void w4a16_stream_pair_kernel(
-    const PT P, const uint16_t* __restrict__ X, int K, int M) {
-  extern __shared__ u32x4_t xs[];
-  constexpr int PPU = kUnit / HG;  // pieces per 8-group unit
-  const int G = K >> 7;
-  const int lane = threadIdx.x & 63;
-  const int wave = wave_id();
-  const int i = lane & 15, a = lane >> 4;
-  const int H = (G + HG - 1) / HG;  // pieces per tile
-  const int ntiles = P.ntiles;
-  const int npairs = (ntiles + 1) >> 1;
-  const int stride = static_cast<int>(gridDim.x) * WV;
-  int p = static_cast<int>(blockIdx.x) * WV + wave;
-  const bool active = p < npairs;
-
-  StageBatch sb0;
-  stage_load(sb0, X, K, 0, M, 0, K, 0);
-  // Three piece buffers: the loads run two pieces ahead of the compute, so
-  // two pieces (both tiles) are in flight while one is multiplied.
-  StreamPiece<HG> bufA[2], bufB[2], bufC[2];
-  const int p0 = min(p, npairs - 1);
-  TileAddr al[2];  // lane addresses of the pair being loaded
-#pragma unroll
-  for (int k = 0; k < 2; ++k) al[k] = tile_addr<PACKED>(P, K, G, min(2 * p0 + k, ntiles - 1), lane);
-  // load position: pair lp, piece lh (the first two pieces are issued here)
-  int lp = p, lh = 0;
-  auto load_next = [&](StreamPiece<HG>(&dst)[2]) {
-    const bool live = lp < npairs;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      TileAddr ad = al[k];
-      // past the last piece, load from the sink instead of branching around the loads
-      if (!live) ad.w = g_piece_sink + lane * 16;
-      stream_load_piece<HG, PACKED, SVEC, FULL>(dst[k], ad, G, (live ? lh : 0) * HG);
-    }
-    if (++lh == H) {
-      lh = 0;
-      lp += stride;
-      if (lp < npairs) {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) al[k] = tile_addr<PACKED>(P, K, G, min(2 * lp + k, ntiles - 1), lane);
-      }
-    }
-  };
-  load_next(bufA);
-  load_next(bufB);
-  const u32x4_t* xrow[CT];
-  const float* corr = stream_prologue<CT, Act, false>(xs, xrow, X, K, M, wave, i, a, sb0);
-  if (!active) return;
-
-  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f32x4_t part[2][CT], total[2][CT];
-#pragma unroll
-  for (int k = 0; k < 2; ++k)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) part[k][ct] = total[k][ct] = zero;
-  int h = 0;
-  const int p_first = p;
-  bool nan_seen = false;
-  using L = Layout<Act, PACKED>;
-  // One piece of the current pair: issue the loads two pieces ahead into
-  // the buffer the previous step consumed, then multiply `cur`.
-  auto step = [&](const StreamPiece<HG>(&cur)[2], StreamPiece<HG>(&ld)[2]) {
-    load_next(ld);
-    const int g0 = h * HG;
-#pragma unroll
-    for (int gg = 0; gg < HG; ++gg) {
-      if (FULL || gg < G - g0) {
-        const int g = g0 + gg;
-        u32x4_t xa[CT][4];
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) load_group_x(xa[ct], xrow[ct] + g * 16, a);
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          f32x4_t t[CT];
-          group_tmp_x<NR, CT, L, false>(t, xa, cur[k].w[gg], corr + g * 16 * CT, a);
-          const float sc = half_bits_to_f32((cur[k].s[gg >> 1] >> (16 * (gg & 1))) & 0xFFFFu);
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-            for (int r = 0; r < NR; ++r) part[k][ct][r] = __builtin_fmaf(sc, t[ct][r], part[k][ct][r]);
-        }
-      }
-    }
-    // an 8-group unit ends after its last piece or at the tile's last piece
-    if ((h % PPU) == PPU - 1 || h == H - 1) {
-#pragma unroll
-      for (int k = 0; k < 2; ++k)
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          total[k][ct] = total[k][ct] + part[k][ct];
-          part[k][ct] = zero;
-        }
-    }
-    if (h == H - 1) {
-#pragma unroll
-      for (int k = 0; k < 2; ++k)
-        if (2 * p + k < ntiles) nan_seen |= store_tile_fast<NR, CT, Act, PT>(P, 2 * p + k, total[k], M, i, a);
-#pragma unroll
-      for (int k = 0; k < 2; ++k)
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) total[k][ct] = zero;
-    }
-    if (++h == H) {
-      h = 0;
-      p += stride;
-    }
-    return p < npairs;
-  };
-  while (step(bufA, bufC) && step(bufB, bufA) && step(bufC, bufB)) {
-  }
-  if (__builtin_expect(__builtin_amdgcn_ballot_w64(nan_seen) != 0, 0)) {
-    // a NaN sum (infinite or NaN activations, overflow): those outputs are
-    // recomputed by the reference loop, which keeps its semantics
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
-    for (int pp = p_first; pp < npairs; pp += stride)
-      for (int k = 0; k < 2; ++k)
-        if (2 * pp + k < ntiles) fix_tile<NR, CT, Act, PT, PACKED>(P, 2 * pp + k, M, i, a, X, K);
   }
 }
 
@@ -1782,12 +1653,14 @@ size_t split_lds_bytes(int K, int M) {
 bool split_fits(int K, int M) { return M <= 32 && split_lds_bytes(K, M) <= kLdsMax; }
 
 // Resident workgroups per CU of the persistent stream kernels: 3 of the
-// 4-wave one-column-tile kernel, 2 of the 8-wave two-column-tile kernel, 1
-// of the 8-wave pair kernel (measured best on the LM head; the alternatives
-// are recorded in the design notes).
+// 4-wave one-column-tile kernel, 2 of the 8-wave two-column-tile kernel
+// (measured best on the LM head). A variant streaming two adjacent weight
+// tiles per wave for M > 16 (each activation fragment read from LDS feeds
+// both tiles' MFMAs) holds ~230 VGPRs, so 8 waves per CU; with the
+// conflict-free activation layout the one-tile kernel's 16 waves per CU are
+// 0.8-1.6 us faster at M = 17..32 on the LM head, so the variant was removed.
 constexpr int kStreamWgsPerCu = 3;
 constexpr int kStreamWideWgsPerCu = 2;
-constexpr int kPairWaves = 8;
 
 template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16>
 int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
@@ -1812,23 +1685,6 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   // 4.30 -> 4.10 us); waves that stream many tiles share the table (inline
   // chains cost the LM head 0.9 us at M = 1 and 3.6 us at M = 8).
   const bool ioff = ntiles <= grid * WV;
-  // two column tiles of one projection: the pair kernel, 8 waves, one
-  // workgroup per CU
-  if constexpr (CT == 2) {
-    if (P.count == 1) {
-      const ProjOne one = shrink_table<1>(P);
-      const int npairs = (ntiles + 1) / 2;
-      auto kern = G % 4 == 0
-                      ? w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, true, kPairWaves, ProjOne>
-                      : w4a16_stream_pair_kernel<PACKED, NR, SVEC, CT, Act, 4, false, kPairWaves, ProjOne>;
-      if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-      const int pwant = (npairs + kPairWaves - 1) / kPairWaves;
-      const int pcap = cu_count();
-      hipLaunchKernelGGL(kern, dim3(pwant < pcap ? pwant : pcap), dim3(kPairWaves * 64), lds, stream,
-                         one, X, K, M);
-      return launch_status();
-    }
-  }
   auto go = [&](const auto& T) {
     using PT = std::decay_t<decltype(T)>;
     auto kern =

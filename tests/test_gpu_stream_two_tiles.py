@@ -1,8 +1,8 @@
-"""The pair stream kernel (17 <= M <= 32, one projection, two 16-row tiles
-per wave) on the LM head and census-like shapes: prepacked and file layout
-equal the tile kernel bit for bit (the per-output operation sequence every
-kernel shares) and are within the oracle's bound; the fp16-activation twin
-through the same kernel, both layouts."""
+"""The stream kernel with two 16-row activation tiles (17 <= M <= 32, one
+projection) on the LM head and census-like shapes: prepacked and file
+layout equal the tile kernel bit for bit (the per-output operation sequence
+every kernel shares) and are within the oracle's bound; the
+fp16-activation twin through the same kernel, both layouts."""
 import numpy as np
 import pytest
 import torch
@@ -17,7 +17,7 @@ def _bits(t):
 
 
 @pytest.mark.parametrize("N,M", SHAPES)
-def test_pair_kernel(w4, orc, dev, N, M):
+def test_two_tile_stream(w4, orc, dev, N, M):
     K = 1024
     W, S = orc.synth_w4a16(0x5A1 + N + M, N, K)
     X = orc.synth_act(0x5A2 + M, M, K)
@@ -37,10 +37,10 @@ def test_pair_kernel(w4, orc, dev, N, M):
     if N <= 4096:
         ok, st = orc.check_tolerance(Y, W, S, X, N, K, M)
         assert ok, (N, M, st)
-        print(f"  pair kernel N={N} M={M}: max {st['max_ulp']:.3f} ulp", flush=True)
+        print(f"  two-tile stream N={N} M={M}: max {st['max_ulp']:.3f} ulp", flush=True)
 
 
-def test_pair_kernel_f16(w4, orc, dev):
+def test_two_tile_stream_f16(w4, orc, dev):
     N, K, M = 4096, 1024, 32
     W, S = orc.synth_w4a16(0x5F16, N, K)
     rng = np.random.default_rng(0x5F16)

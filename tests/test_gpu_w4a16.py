@@ -447,12 +447,12 @@ def test_piece_split_equals_stream(w4, orc, dev, N, K, M):
 @pytest.mark.parametrize("N,bad", [(100003, False), (100002, False), (40000, False), (100008, False),
                                    (100008, True)])
 @pytest.mark.parametrize("M", [17, 24, 31, 32])
-def test_pair_kernel_edges(w4, orc, dev, N, bad, M):
-    # the pair kernel (one projection, M = 17..32, many tiles) against the
-    # tile kernel bit for bit: odd and even N, ragged last tiles and pairs,
-    # masked rows (M < 32), y at an odd element, an infinite activation (the
-    # reference loop's +-Inf / NaN outputs), and the element past y left
-    # untouched
+def test_two_tile_stream_edges(w4, orc, dev, N, bad, M):
+    # the stream kernel with two activation tiles (one projection, M =
+    # 17..32, many tiles) against the tile kernel bit for bit: odd and even
+    # N, ragged last tiles, masked rows (M < 32), y at an odd element, an
+    # infinite activation (the reference loop's +-Inf / NaN outputs), and
+    # the element past y left untouched
     K = 1024
     W, S = orc.synth_w4a16(0x9A1 + N, N, K)
     X = orc.synth_act(0x9A2 + M, M, K)
