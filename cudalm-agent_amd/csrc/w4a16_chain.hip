@@ -43,7 +43,8 @@
 //     start (+1) and stored back by the last workgroup to exit, which it
 //     learns from two levels of exit counters (reset by their last member),
 //     so no flag is ever cleared and a replay needs no memset;
-//   * every wait is bounded (~0.5 s of s_memrealtime) and gives up at once
+//   * every wait is bounded (~0.5 s of s_memrealtime by default, settable
+//     with cudalm_w4a16_chain_set_wait_bound) and gives up at once
 //     when another wait has failed: it then sets the workspace error word
 //     and the stage proceeds, so every wave exits; the host reads the word
 //     with cudalm_w4a16_chain_status.
@@ -92,8 +93,10 @@ constexpr int kChainFlagStride = 32;  // u32 words between flags: one 128-byte l
 constexpr size_t kChainHeader = 1024;
 
 // Workspace: [header 1 KB][stage table, 256 B per stage][flags, 32 KB per stage]
-// header words (byte offsets): epoch 0, error 64, exit_top 128, exit_sub[j] 256 + 64 j.
-constexpr size_t kEpochOff = 0, kErrorOff = 64, kExitTopOff = 128, kExitSubOff = 256;
+// header words (byte offsets): epoch 0, error 64, exit_top 128, wait bound 192,
+// exit_sub[j] 256 + 64 j.
+constexpr size_t kEpochOff = 0, kErrorOff = 64, kExitTopOff = 128, kBoundOff = 192, kExitSubOff = 256;
+constexpr uint32_t kDefaultWaitTicks = 50000000u;  // ~0.5 s of s_memrealtime (100 MHz)
 constexpr int kExitSubs = 8;
 
 struct alignas(256) ChainStage {
@@ -172,7 +175,7 @@ __device__ __forceinline__ StageProj stage_proj(const ChainStage& S, int t) {
 // 0.95 us). Lane l polls workgroups l, l+64, l+128, l+192 with
 // device-coherent loads. Returns false on a timeout (after posting the
 // error) or when another wait already failed.
-__device__ bool chain_wait(const uint32_t* flags, int n, uint32_t e, uint32_t* err) {
+__device__ bool chain_wait(const uint32_t* flags, int n, uint32_t e, uint32_t* err, uint32_t ticks) {
   const int lane = threadIdx.x & 63;
   long long deadline = 0;
   for (int it = 0;; ++it) {
@@ -187,7 +190,7 @@ __device__ bool chain_wait(const uint32_t* flags, int n, uint32_t e, uint32_t* e
       if (ld_dev_u32(err) != 0) return false;  // another wait has failed: give up at once
       const long long now = __builtin_amdgcn_s_memrealtime();
       if (deadline == 0) {
-        deadline = now + 50000000LL;  // ~0.5 s at 100 MHz
+        deadline = now + static_cast<long long>(ticks);
       } else if (now > deadline) {
         if (lane == 0) __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return false;
@@ -211,7 +214,7 @@ size_t chain_lds_bytes(int M, int gt) {
 template <bool PACKED, int NR, int CT, int GPW>
 __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M, int gt_max,
                                             f32x4_t* lds_park, uint32_t* flags, uint32_t e,
-                                            uint32_t* err) {
+                                            uint32_t* err, uint32_t ticks) {
   using Park = typename std::conditional<NR == 1, float, f32x4_t>::type;
   constexpr int kChainFrag = chain_frag(GPW, CT);
   const int lane = threadIdx.x & 63;
@@ -277,7 +280,8 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
       // first round: wait for the stage x depends on, then x and the offsets
       have_x = true;
       if (S.dep >= 0) {
-        if (wave == 0) chain_wait(flags + S.dep * kChainFlagSlots * kChainFlagStride, S.dep_nwg, e, err);
+        if (wave == 0)
+          chain_wait(flags + S.dep * kChainFlagSlots * kChainFlagStride, S.dep_nwg, e, err, ticks);
         __syncthreads();
       }
       const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(S.x);
@@ -398,9 +402,14 @@ __global__ __launch_bounds__(kChainWaves * 64) void w4a16_chain_kernel(
   uint32_t* err = reinterpret_cast<uint32_t*>(hdr + kErrorOff);
   const int nwgs = static_cast<int>(gridDim.x);
   const int b = static_cast<int>(blockIdx.x);
-  if (threadIdx.x == 0) *sh_epoch = ld_dev_u32(reinterpret_cast<uint32_t*>(hdr + kEpochOff)) + 1u;
+  if (threadIdx.x == 0) {
+    sh_epoch[0] = ld_dev_u32(reinterpret_cast<uint32_t*>(hdr + kEpochOff)) + 1u;
+    const uint32_t b = ld_dev_u32(reinterpret_cast<uint32_t*>(hdr + kBoundOff));
+    sh_epoch[1] = b != 0 ? b : kDefaultWaitTicks;
+  }
   __syncthreads();
-  const uint32_t e = __builtin_amdgcn_readfirstlane(*sh_epoch);
+  const uint32_t e = __builtin_amdgcn_readfirstlane(sh_epoch[0]);
+  const uint32_t ticks = __builtin_amdgcn_readfirstlane(sh_epoch[1]);
 
   for (int s = 0; s < nst; ++s) {
     const ChainStage& S = table[s];
@@ -409,11 +418,11 @@ __global__ __launch_bounds__(kChainWaves * 64) void w4a16_chain_kernel(
     if (slot >= S.nwg) continue;
     const int G = S.K >> 7;
     if (G <= kChainWaves)
-      chain_stage<PACKED, NR, CT, 1>(S, slot, M, gt_max, lds_park, flags, e, err);
+      chain_stage<PACKED, NR, CT, 1>(S, slot, M, gt_max, lds_park, flags, e, err, ticks);
     else if (G <= 2 * kChainWaves)
-      chain_stage<PACKED, NR, CT, 2>(S, slot, M, gt_max, lds_park, flags, e, err);
+      chain_stage<PACKED, NR, CT, 2>(S, slot, M, gt_max, lds_park, flags, e, err, ticks);
     else
-      chain_stage<PACKED, NR, CT, 4>(S, slot, M, gt_max, lds_park, flags, e, err);
+      chain_stage<PACKED, NR, CT, 4>(S, slot, M, gt_max, lds_park, flags, e, err, ticks);
     if (threadIdx.x == 0) st_dev_u32(flags + (s * kChainFlagSlots + slot) * kChainFlagStride, e);
   }
 
@@ -636,6 +645,16 @@ int cudalm_w4a16_chain_status(const cudalm_w4a16_chain* chain, hipStream_t strea
   if (word == 0) return CUDALM_W4A16_OK;
   if (hipMemset(errp, 0, sizeof(word)) != hipSuccess) return CUDALM_W4A16_ELAUNCH;
   return CUDALM_W4A16_ETIMEOUT;
+}
+
+int cudalm_w4a16_chain_set_wait_bound(const cudalm_w4a16_chain* chain, uint32_t ticks,
+                                      hipStream_t stream) {
+  if (!chain || !chain->workspace) return CUDALM_W4A16_ENULL;
+  uint8_t* bp = static_cast<uint8_t*>(chain->workspace) + kBoundOff;
+  if (hipMemcpyAsync(bp, &ticks, sizeof(ticks), hipMemcpyHostToDevice, stream) != hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess)
+    return CUDALM_W4A16_ELAUNCH;
+  return CUDALM_W4A16_OK;
 }
 
 int cudalm_w4a16_gemv_bf16_chain(const cudalm_w4a16_stage* stages, int n_stages, int M,

@@ -73,6 +73,7 @@ _SIGS = {
     "cudalm_w4a16_chain_plan": ([_P, _I, _I, _I, _P, _SZ, _P, _P], _I),
     "cudalm_w4a16_chain_run": ([_P, _P], _I),
     "cudalm_w4a16_chain_status": ([_P, _P], _I),
+    "cudalm_w4a16_chain_set_wait_bound": ([_P, ctypes.c_uint32, _P], _I),
     "cudalm_w4a16_gemv_bf16_chain": ([_P, _I, _I, _I, _P, _SZ, _P], _I),
     "cudalm_w4a16_gemv_bf16_chain_noalloc": ([_P, _I, _I, _I, _P], _I),
 }
@@ -354,6 +355,13 @@ class Chain:
     def status(self, stream=None) -> None:
         _check(_lib.cudalm_w4a16_chain_status(ctypes.byref(self.handle), _stream(stream)),
                "cudalm_w4a16_chain_status")
+
+    def set_wait_bound(self, ticks: int, stream=None) -> None:
+        """Bound of every wait of later runs, in 100 MHz s_memrealtime ticks
+        (0 = the default, ~0.5 s)."""
+        _check(_lib.cudalm_w4a16_chain_set_wait_bound(ctypes.byref(self.handle), ticks,
+                                                      _stream(stream)),
+               "cudalm_w4a16_chain_set_wait_bound")
 
 
 # ---------------------------------------------------------------------------

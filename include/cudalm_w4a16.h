@@ -158,6 +158,15 @@ int cudalm_w4a16_chain_run(const cudalm_w4a16_chain* chain, hipStream_t stream);
 /* Synchronizes `stream`, then returns CUDALM_W4A16_ETIMEOUT (and clears
  * the record) if a wait of a run since the last call timed out, else 0. */
 int cudalm_w4a16_chain_status(const cudalm_w4a16_chain* chain, hipStream_t stream);
+/* Sets the bound of every wait of later runs of `chain`, in ticks of the
+ * 100 MHz s_memrealtime counter (0 = the default, about 0.5 s), and
+ * synchronizes `stream`; a new plan resets it to the default. A wait past
+ * its bound gives up (its stage proceeds and every wave exits) and
+ * cudalm_w4a16_chain_status then reports CUDALM_W4A16_ETIMEOUT. For callers
+ * that prefer an early error to a long stall, and for tests of the timeout
+ * path. No counterpart in the reference. */
+int cudalm_w4a16_chain_set_wait_bound(const cudalm_w4a16_chain* chain, uint32_t ticks,
+                                      hipStream_t stream);
 /* plan + run in one call (not capturable: the plan synchronizes). */
 int cudalm_w4a16_gemv_bf16_chain(const cudalm_w4a16_stage* stages, int n_stages, int M,
                                  int prepacked, void* workspace, size_t workspace_bytes,

@@ -214,3 +214,37 @@ def test_chain_infinite_activation(orc, w4, dev):
     r = orc.gemv_bf16(W, S, X, N, K, M)
     assert np.array_equal(np.isinf(orc.bf16_to_f32(_bits(y).reshape(M, N)[2])),
                           np.isinf(orc.bf16_to_f32(r[2])))
+
+
+def test_chain_wait_bound_timeout(orc, w4, dev):
+    """The timeout path, forced from the host: 48 one-tile stages, each
+    waiting for the previous one, so the last stages' workgroups wait ~100 us
+    from the launch; with a wait bound of 1 tick those waits give up (their
+    stages proceed and every wave exits), status() reports the timeout once
+    and clears it; with the default bound restored the same chain runs clean
+    and gives the outputs of per-stage launches."""
+    N, K, M, S = 16, 1024, 1, 48
+    W, Sc = orc.synth_w4a16(0xC4A1B000, N, K)
+    X = orc.synth_act(0xC4A1B001, M, K)
+    w = torch.from_numpy(W).to(dev)
+    s = torch.from_numpy(Sc.view(np.int16)).to(dev).view(torch.float16)
+    x = torch.from_numpy(X.view(np.int16)).to(dev).view(torch.bfloat16)
+    p = w4.repack(w, s, N, K)
+    ys = [torch.empty((M, N), dtype=torch.bfloat16, device=dev) for _ in range(S)]
+    chain = w4.Chain([([(p.data_ptr(), None, ys[k].data_ptr(), N)], x, K, k - 1) for k in range(S)],
+                     M, prepacked=True)
+    chain.set_wait_bound(1)
+    chain.run()
+    with pytest.raises(w4.W4A16Error) as ei:
+        chain.status()
+    assert ei.value.code == w4.ETIMEOUT
+    chain.status()  # the record was cleared
+    chain.set_wait_bound(0)
+    for y in ys:
+        y.fill_(float("nan"))
+    chain.run()
+    chain.status()
+    ref = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    w4.gemv_prepacked(p, x, N, K, M, y=ref)
+    for y in ys:
+        assert np.array_equal(_bits(y), _bits(ref))
