@@ -21,6 +21,12 @@
 //   gate.bin, up.bin     bf16[M][N]  w4a16_forward_bf16 of the gate / up linears
 //   silu_mul.bin         bf16[M][N]  kernels::qwen35_silu_mul_bf16(gate, up)
 //   swiglu.bin           bf16[M][N]  w4a16_swiglu_forward_bf16 (one launch)
+//   chain_gate.bin, chain_up.bin, chain_w.bin   bf16[M][N]  a two-stage chain
+//                        over the C ABI (gate + up, then the W linear
+//                        waiting for it): cudalm_w4a16_chain_plan / _run /
+//                        _status
+//   noalloc_w.bin        bf16[M][N]  the same chain through
+//                        cudalm_w4a16_gemv_bf16_chain_noalloc
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -35,6 +41,7 @@
 #include "cudalm/kernels/int4_gemv_bf16.h"
 #include "cudalm/kernels/swiglu.h"
 #include "cudalm/w4a16_linear.h"
+#include "cudalm_w4a16.h"
 
 namespace {
 
@@ -164,7 +171,33 @@ int main(int argc, char** argv) {
   cudalm::kernels::qwen35_silu_mul_bf16(yg, yu, ysm, static_cast<std::size_t>(M) * N, stream);
   cudalm::w4a16_swiglu_forward_bf16(gate, up, X, ysw, M, stream);
 
+  // stage chains (C ABI): gate and up as one stage, then the W linear
+  // waiting for it; then the same stages without a workspace
+  auto* ycg = device<std::uint16_t>(yb);
+  auto* ycu = device<std::uint16_t>(yb);
+  auto* ycw = device<std::uint16_t>(yb);
+  auto* ycn = device<std::uint16_t>(yb);
+  {
+    const auto* xs = reinterpret_cast<const std::uint16_t*>(X);
+    const cudalm_w4a16_proj gu[2] = {{gate.packed, nullptr, ycg, N}, {up.packed, nullptr, ycu, N}};
+    const cudalm_w4a16_proj lw[1] = {{lin_d.packed, nullptr, ycw, N}};
+    const cudalm_w4a16_proj ln[1] = {{lin_d.packed, nullptr, ycn, N}};
+    const cudalm_w4a16_stage stages[2] = {{gu, 2, xs, K, -1}, {lw, 1, xs, K, 0}};
+    const cudalm_w4a16_stage stages_n[2] = {{gu, 2, xs, K, -1}, {ln, 1, xs, K, 0}};
+    const std::size_t wsb = cudalm_w4a16_chain_workspace_bytes(2);
+    void* ws = device<void>(wsb);
+    cudalm_w4a16_chain chain;
+    if (cudalm_w4a16_chain_plan(stages, 2, M, 1, ws, wsb, &chain, stream) != 0) die("chain plan");
+    if (cudalm_w4a16_chain_run(&chain, stream) != 0) die("chain run");
+    if (cudalm_w4a16_chain_status(&chain, stream) != 0) die("chain status");
+    if (cudalm_w4a16_gemv_bf16_chain_noalloc(stages_n, 2, M, 1, stream) != 0) die("chain noalloc");
+  }
+
   hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  download("chain_gate.bin", ycg, yb);
+  download("chain_up.bin", ycu, yb);
+  download("chain_w.bin", ycw, yb);
+  download("noalloc_w.bin", ycn, yb);
   download("int4_gemv_bf16.bin", y1, static_cast<std::size_t>(N) * 2);
   download("batch.bin", yB, yb);
   download("forward_host.bin", yF, yb);

@@ -3,8 +3,9 @@ calls it: tests/cpp/boundary_check (built by build(), compiled against
 include/cudalm/ and linked with libcudalm_w4a16.so) runs
 cudalm::int4_gemv_bf16, kernels::batch_int4_gemv_bf16, repack_w4a16_host /
 repack_w4a16 -> w4a16_forward_bf16, bf16_gemv, kernels::batch_bf16_gemv,
-int4_gemv, kernels::qwen35_silu_mul_bf16 and w4a16_swiglu_forward_bf16 on
-device buffers (reference headers: include/cudalm/kernels/int4_gemv_bf16.h:46-52,
+int4_gemv, kernels::qwen35_silu_mul_bf16 and w4a16_swiglu_forward_bf16, and
+a two-stage chain over the C ABI (cudalm_w4a16_chain_* and the allocation-free
+entry), on device buffers (reference headers: include/cudalm/kernels/int4_gemv_bf16.h:46-52,
 batch_decode.h:61-79, bf16_gemv.h:19-38, int4_gemv.h:22-40,
 qwen35_kernels.h:146-155; weight_loader.h:58-63). Inputs and outputs pass
 through files; every output is checked here against the CPU oracle."""
@@ -79,3 +80,9 @@ def test_cpp_boundary(orc, tmp_path, N, K, M):
     dd = _ulp_diff(sm, orc.silu_mul_bf16(g, u))
     assert dd.max() <= 1 and (dd != 0).sum() * 1000 <= dd.size, (int(dd.max()), int((dd != 0).sum()))
     assert np.array_equal(out("swiglu", M), sm)
+    # stage chains over the C ABI, and the allocation-free entry: the bits of
+    # the per-projection calls
+    assert np.array_equal(out("chain_gate", M), g)
+    assert np.array_equal(out("chain_up", M), u)
+    assert np.array_equal(out("chain_w", M), yB)
+    assert np.array_equal(out("noalloc_w", M), yB)
