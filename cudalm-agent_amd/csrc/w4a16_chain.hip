@@ -104,6 +104,7 @@ struct alignas(256) ChainStage {
   const uint16_t* s[kChainProj];
   uint16_t* y[kChainProj];
   const uint16_t* x;
+  uint16_t* act;  // SwiGLU epilogue output, or null
   int n[kChainProj];
   int tile_end[kChainProj];
   int count, K, dep, ntiles;
@@ -144,7 +145,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) 
 }
 
 // The projection that owns stage tile t: every field is read at a constant
-// offset and picked with selects (no data-dependent scalar load chain).
+// offset and picked with selects (no data-dependent scalar load chain). A
+// SwiGLU stage interleaves its two projections (tile t is row tile t / 2 of
+// gate for even t, of up for odd t), so a workgroup's round holds whole
+// gate/up pairs.
 struct StageProj {
   const uint8_t* w;
   const uint16_t* s;
@@ -155,6 +159,14 @@ struct StageProj {
 
 __device__ __forceinline__ StageProj stage_proj(const ChainStage& S, int t) {
   StageProj v = {S.w[0], S.s[0], S.y[0], S.n[0], 0};
+  if (S.act != nullptr) {
+    if (t & 1) {
+      v.w = S.w[1];
+      v.s = S.s[1];
+    }
+    v.begin = t - (t >> 1);
+    return v;
+  }
 #pragma unroll
   for (int k = 1; k < kChainProj; ++k) {
     if (k < S.count && t >= S.tile_end[k - 1]) {
@@ -201,10 +213,14 @@ __device__ bool chain_wait(const uint32_t* flags, int n, uint32_t e, uint32_t* e
 
 // Park area of one round: tile j, group g, column tile ct at
 // [(j * G + g) * CT + ct][64 lanes] (NR == 1 parks one float per lane, row 0
-// being the only output row; else a f32x4), then 16 scales per (j, g).
+// being the only output row; else a f32x4), then 16 scales per (j, g), then
+// the SwiGLU exchange: the bf16 up outputs of up to kChainPairs gate/up tile
+// pairs, [pair][ct * NR + r][64 lanes] u32.
+constexpr int kChainPairs = 2;
 size_t chain_lds_bytes(int M, int gt) {
   const int NR = M == 1 ? 1 : 4, CT = M > 16 ? 2 : 1;
-  return 16 + static_cast<size_t>(gt) * (static_cast<size_t>(CT) * 64 * (NR == 1 ? 4 : 16) + 64);
+  return 16 + static_cast<size_t>(gt) * (static_cast<size_t>(CT) * 64 * (NR == 1 ? 4 : 16) + 64) +
+         static_cast<size_t>(kChainPairs) * CT * NR * 64 * 4;
 }
 
 // One stage of the chain for one workgroup (slot = its index among the
@@ -229,6 +245,7 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
   const int U = (G + kUnit - 1) / kUnit;
   Park* tmps = reinterpret_cast<Park*>(lds_park);
   float* scs = reinterpret_cast<float*>(tmps + static_cast<size_t>(gt_max) * CT * 64);
+  uint32_t* xch = reinterpret_cast<uint32_t*>(scs + static_cast<size_t>(gt_max) * 16);
   // this wave's activation fragments and offset chains, per owned group
   u32x4_t xa[GPW][CT][4];
   f32x4_t off[GPW][CT];
@@ -332,12 +349,12 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
       }
     }
     __syncthreads();
-    if (wave < tn) {
-      // tile t0 + wave: the canonical chain over the parked group results
-      const int j = wave;
-      f32x4_t total[CT];
+    // tile t0 + wave: the canonical chain over the parked group results
+    const int j = wave;
+    f32x4_t total[CT];
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
+    for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
+    if (wave < tn) {
       for (int u = 0; u < U; ++u) {
         f32x4_t p[CT];
 #pragma unroll
@@ -360,30 +377,57 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) total[ct] = total[ct] + p[ct];
       }
-      const int t = t0 + j;
-      const StageProj v = stage_proj(S, t);
-      const int Nj = v.n;
-      const int n = (t - v.begin) * kTileRows + i;
-      if (n < Nj) {
-        uint16_t* col = v.y + n;
+    }
+    const int t = t0 + j;
+    const StageProj v = stage_proj(S, t);
+    const int Nj = v.n;
+    const int n = (t - v.begin) * kTileRows + i;
+    // y bits of (ct, r) for this lane's column n; a NaN sum (infinite or NaN
+    // activations, overflow) is recomputed by the reference loop, keeping
+    // its semantics
+    auto out_bits = [&](int ct, int r, int m) -> uint32_t {
+      float val = 16.0f * total[ct][r];
+      if (__builtin_expect(val != val, 0))
+        val = w4a16_ref_dot<PACKED, false, true>(v.w, v.s, K, n, S.x + static_cast<size_t>(m) * K);
+      return f32_to_bf16_rne(val);
+    };
+    if (S.act != nullptr) {
+      // SwiGLU: the up wave of each pair parks its bf16 outputs, then the
+      // gate wave writes act = silu(gate) * up
+      uint32_t* px = xch + static_cast<size_t>(j >> 1) * CT * NR * 64;
+      if (wave < tn && (j & 1) && n < Nj) {
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
           for (int r = 0; r < NR; ++r) {
             const int m = ct * 16 + 4 * a + r;
-            if (m < M) {
-              // a NaN sum (infinite or NaN activations, overflow) is
-              // recomputed by the reference loop, keeping its semantics
-              float val = 16.0f * total[ct][r];
-              if (__builtin_expect(val != val, 0))
-                val = w4a16_ref_dot<PACKED, false, true>(v.w, v.s, K, n, S.x + static_cast<size_t>(m) * K);
-              st_dev_u16(col + static_cast<size_t>(m) * Nj,
-                         static_cast<uint16_t>(f32_to_bf16_rne(val)));
-            }
+            if (m < M) px[(ct * NR + r) * 64 + lane] = out_bits(ct, r, m);
           }
       }
-      __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
+      __syncthreads();
+      if (wave < tn && !(j & 1) && n < Nj) {
+        uint16_t* col = S.act + n;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            const int m = ct * 16 + 4 * a + r;
+            if (m < M)
+              st_dev_u16(col + static_cast<size_t>(m) * Nj,
+                         static_cast<uint16_t>(silu_mul_bits(out_bits(ct, r, m), px[(ct * NR + r) * 64 + lane])));
+          }
+      }
+    } else if (wave < tn && n < Nj) {
+      uint16_t* col = v.y + n;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const int m = ct * 16 + 4 * a + r;
+          if (m < M) st_dev_u16(col + static_cast<size_t>(m) * Nj, static_cast<uint16_t>(out_bits(ct, r, m)));
+        }
     }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
     __syncthreads();  // every store of the round is complete; the park area is free
   }
 }
@@ -538,6 +582,20 @@ void* scratch_ptr() {
   return p;
 }
 
+// A stage's workgroups (nwg, at most max_wg) and tiles per workgroup and
+// round (tpw, at most what the registers hold). A SwiGLU stage takes an
+// even tpw (4 or 2 fit: K <= 2048), so every round holds whole pairs.
+void chain_split(ChainStage& T, int M, int max_wg) {
+  const int G = T.K / kGroup;
+  const int tcap = chain_frag(chain_gpw(G), M > 16 ? 2 : 1) / chain_gpw(G);
+  const int nwg = (T.ntiles + tcap - 1) / tcap;
+  T.nwg = nwg < max_wg ? nwg : max_wg;
+  T.tpw = (T.ntiles + T.nwg - 1) / T.nwg;
+  if (T.act != nullptr) T.tpw = (T.tpw + 1) & ~1;
+  if (T.tpw > tcap) T.tpw = tcap;
+  if (T.act != nullptr) T.nwg = std::min(max_wg, (T.ntiles + T.tpw - 1) / T.tpw);
+}
+
 // The plan, written into `workspace` from the host table `tab` (n_stages
 // entries, filled here).
 int chain_plan_into(const cudalm_w4a16_stage* stages, int n_stages, int M, int prepacked,
@@ -560,12 +618,21 @@ int chain_plan_into(const cudalm_w4a16_stage* stages, int n_stages, int M, int p
       return CUDALM_W4A16_EINVAL;
     if (st.dep < -1 || st.dep >= s) return CUDALM_W4A16_EINVAL;
     if (!aligned(st.x, 16)) return CUDALM_W4A16_EALIGN;
+    const bool epi = st.act != nullptr;
+    if (epi) {
+      // SwiGLU: gate and up of one shape, at most two groups per wave so a
+      // round holds whole tile pairs
+      if (st.count != 2 || st.projs[0].N != st.projs[1].N || st.K > 2 * kChainWaves * kGroup)
+        return CUDALM_W4A16_EINVAL;
+      if (!aligned(st.act, 2)) return CUDALM_W4A16_EALIGN;
+    }
     int tiles = 0;
     for (int j = 0; j < st.count; ++j) {
       const cudalm_w4a16_proj& p = st.projs[j];
       if (p.N < 1 || p.N > (1 << 24)) return CUDALM_W4A16_EINVAL;
-      if (!p.weight || !p.y || (!prepacked && !p.scale)) return CUDALM_W4A16_ENULL;
-      if (!aligned(p.weight, 16) || !aligned(p.y, 2) || (!prepacked && !aligned(p.scale, 2)))
+      if (!p.weight || (!epi && !p.y) || (!prepacked && !p.scale)) return CUDALM_W4A16_ENULL;
+      if (!aligned(p.weight, 16) || (!epi && !aligned(p.y, 2)) ||
+          (!prepacked && !aligned(p.scale, 2)))
         return CUDALM_W4A16_EALIGN;
       T.w[j] = static_cast<const uint8_t*>(p.weight);
       T.s[j] = p.scale;
@@ -576,17 +643,13 @@ int chain_plan_into(const cudalm_w4a16_stage* stages, int n_stages, int M, int p
     }
     if (static_cast<long long>(M) * st.K > (1LL << 30)) return CUDALM_W4A16_ERANGE;
     T.x = st.x;
+    T.act = st.act;
     T.count = st.count;
     T.K = st.K;
     T.dep = st.dep;
     T.ntiles = tiles;
-    const int G = st.K / kGroup;
-    const int tcap = chain_frag(chain_gpw(G), M > 16 ? 2 : 1) / chain_gpw(G);
-    const int nwg = (tiles + tcap - 1) / tcap;
-    T.nwg = nwg < kChainMaxWg ? nwg : kChainMaxWg;
-    T.tpw = (tiles + T.nwg - 1) / T.nwg;
-    if (T.tpw > tcap) T.tpw = tcap;
-    if (T.tpw * G > gt_max) gt_max = T.tpw * G;
+    chain_split(T, M, kChainMaxWg);
+    if (T.tpw * (st.K / kGroup) > gt_max) gt_max = T.tpw * (st.K / kGroup);
   }
   int occ = 0;
   if (int rc = chain_launch(prepacked, nullptr, n_stages, M, gt_max, &occ, false, stream)) return rc;
@@ -595,13 +658,7 @@ int chain_plan_into(const cudalm_w4a16_stage* stages, int n_stages, int M, int p
   int first = 0;
   for (int s = 0; s < n_stages; ++s) {
     ChainStage& T = tab[static_cast<size_t>(s)];
-    if (T.nwg > grid) {  // fewer resident workgroups than the plan: more rounds
-      T.nwg = grid;
-      const int G = T.K / kGroup;
-      const int tcap = chain_frag(chain_gpw(G), M > 16 ? 2 : 1) / chain_gpw(G);
-      T.tpw = (T.ntiles + grid - 1) / grid;
-      if (T.tpw > tcap) T.tpw = tcap;
-    }
+    if (T.nwg > grid) chain_split(T, M, grid);  // fewer resident workgroups: more rounds
     T.first = first;
     first = (first + T.nwg) % grid;
     T.dep_nwg = T.dep >= 0 ? tab[static_cast<size_t>(T.dep)].nwg : 0;

@@ -830,15 +830,6 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
 // qwen35_deltanet.cpp:236-251, src/kernels/qwen35_kernels.cu:458-476).
 // ---------------------------------------------------------------------------
 
-// y = bf16( f32(bf16(g / (1 + exp(-g)))) * u ) on bf16 inputs g, u: SiLU in
-// fp32, rounded to bf16 first, then the product rounded once
-// (include/cudalm/kernels/qwen35_kernels.h:146-152).
-__device__ __forceinline__ uint32_t silu_mul_bits(uint32_t g_bits, uint32_t u_bits) {
-  const float g = bf16_lo(g_bits);
-  const float s = bf16_lo(f32_to_bf16_rne(g / (1.0f + expf(-g))));
-  return f32_to_bf16_rne(s * bf16_lo(u_bits));
-}
-
 // Element-wise silu(gate) * up over n values; 8 per thread (16 B vectors
 // when the three bases are 16 B aligned, element-wise otherwise).
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gate,

@@ -136,7 +136,7 @@ class Proj(ctypes.Structure):
 class Stage(ctypes.Structure):
     """struct cudalm_w4a16_stage (include/cudalm_w4a16.h)."""
     _fields_ = [("projs", ctypes.c_void_p), ("count", ctypes.c_int), ("x", ctypes.c_void_p),
-                ("K", ctypes.c_int), ("dep", ctypes.c_int)]
+                ("K", ctypes.c_int), ("dep", ctypes.c_int), ("act", ctypes.c_void_p)]
 
 
 class ChainHandle(ctypes.Structure):
@@ -320,23 +320,27 @@ def gemv_multi(weights, scales, x, Ns, K: int, M: int = 1, ys=None, prepacked: b
 class Chain:
     """A planned stage chain (cudalm_w4a16_chain_plan) and its workspace.
 
-    stages: list of (items, x, K, dep) with items a list of
-    (weight_ptr, scale_ptr_or_None, y_ptr, N) sharing x (a tensor or a raw
-    address); dep is the index of an earlier stage or -1. run() is one kernel
-    launch (capturable); status() synchronizes and raises W4A16Error on a
-    timed-out wait."""
+    stages: list of (items, x, K, dep) or (items, x, K, dep, act) with items
+    a list of (weight_ptr, scale_ptr_or_None, y_ptr, N) sharing x (a tensor
+    or a raw address); dep is the index of an earlier stage or -1; act (a
+    tensor or address, or None) makes the stage a SwiGLU stage: items are
+    gate and up, and act = silu(gate(x)) * up(x) is its only output. run()
+    is one kernel launch (capturable); status() synchronizes and raises
+    W4A16Error on a timed-out wait."""
 
     def __init__(self, stages, M: int, prepacked: bool = True, device=None, stream=None):
         import torch
 
-        self._arrays = [proj_array(items) for items, _x, _K, _dep in stages]
+        stages = [tuple(sg) + (None,) * (5 - len(sg)) for sg in stages]
+        self._arrays = [proj_array(sg[0]) for sg in stages]
         st = (Stage * len(stages))()
-        for k, ((items, x, K, dep), arr) in enumerate(zip(stages, self._arrays)):
+        for k, ((items, x, K, dep, act), arr) in enumerate(zip(stages, self._arrays)):
             st[k].projs = ctypes.cast(arr, ctypes.c_void_p)
             st[k].count = len(items)
             st[k].x = x if isinstance(x, int) else _ptr(x)
             st[k].K = K
             st[k].dep = dep
+            st[k].act = act if (act is None or isinstance(act, int)) else _ptr(act)
         self._stages = st
         nbytes = _lib.cudalm_w4a16_chain_workspace_bytes(len(stages))
         if nbytes == 0:

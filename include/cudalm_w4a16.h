@@ -145,6 +145,16 @@ typedef struct cudalm_w4a16_stage {
   const uint16_t* x; /* bf16 [M, K] */
   int K;
   int dep; /* earlier stage that must complete before x is read, or -1 */
+  /* SwiGLU epilogue (NULL = none). When set, the stage has count == 2
+   * projections of equal N, gate then up, and K <= 2048; it writes only
+   *   act[m, n] = bf16( f32(bf16(silu(g))) * f32(u) )   (bf16 [M, N]),
+   * g and u being the bits cudalm_w4a16_gemv_bf16 gives for gate and up,
+   * i.e. what cudalm_w4a16_swiglu_bf16 writes; the projections' y are
+   * ignored (may be NULL). A later stage with dep on this one may read act
+   * as its x: the reference's gate -> up -> qwen35_silu_mul_bf16 -> down
+   * sequence (src/runtime/qwen35_deltanet.cpp:236-251) as two stages of one
+   * launch. No counterpart in the reference. */
+  uint16_t* act;
 } cudalm_w4a16_stage;
 typedef struct cudalm_w4a16_chain { /* filled by cudalm_w4a16_chain_plan */
   void* workspace;

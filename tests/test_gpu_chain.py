@@ -248,3 +248,107 @@ def test_chain_wait_bound_timeout(orc, w4, dev):
     w4.gemv_prepacked(p, x, N, K, M, y=ref)
     for y in ys:
         assert np.array_equal(_bits(y), _bits(ref))
+
+
+def _dev_mat(orc, w4, dev, seed, N, K, prepacked):
+    W, S = orc.synth_w4a16(seed, N, K)
+    w = torch.from_numpy(W).to(dev)
+    s = torch.from_numpy(S.view(np.int16)).to(dev).view(torch.float16)
+    return (w4.repack(w, s, N, K), None) if prepacked else (w, s)
+
+
+@pytest.mark.parametrize("M", [1, 8, 17, 32])
+@pytest.mark.parametrize("prepacked", [True, False])
+def test_chain_swiglu_mlp(orc, w4, dev, M, prepacked):
+    """SwiGLU stages (stage.act): two MLP blocks in one launch, each a
+    gate/up stage writing act = silu(gate) * up and a down stage reading act,
+    the second block overwriting the first block's act and reading its
+    output. Every output bit-identical to cudalm_w4a16_swiglu_bf16 followed
+    by cudalm_w4a16_gemv_bf16, launch by launch. Shapes: the census MLP
+    (3584 x 1024 gate/up), a ragged one at K = 2048 (two groups per wave,
+    1000 rows: 63 tile pairs) and a one-tile one."""
+    print(f"  chain swiglu M={M} prepacked={prepacked}", flush=True)
+    seed = 0xC4A15000 + 31 * M + int(prepacked)
+    blocks = [(3584, 1024), (1000, 2048), (16, 1024)]  # (N of gate/up, K = hidden)
+    mats = []
+    for b, (N, K) in enumerate(blocks):
+        g = _dev_mat(orc, w4, dev, seed + 8 * b, N, K, prepacked)
+        u = _dev_mat(orc, w4, dev, seed + 8 * b + 1, N, K, prepacked)
+        # down: [K, N], only where act's width is whole groups
+        d = _dev_mat(orc, w4, dev, seed + 8 * b + 2, K, N, prepacked) if N % 128 == 0 else None
+        mats.append((g, u, d))
+    X = orc.synth_act(seed + 7, M, 2048)
+    x = torch.from_numpy(X.view(np.int16)).to(dev).view(torch.bfloat16)
+
+    for b, (N, K) in enumerate(blocks):
+        (g, u, d) = mats[b]
+        xk = x[:, :K].contiguous()
+        down = N % 128 == 0
+        # reference: one launch per step
+        act_ref = w4.swiglu(g[0], g[1], u[0], u[1], xk, N, K, M, prepacked=prepacked)
+        h_ref = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+        act2_ref = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        h2_ref = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+        if down:
+            def lin(m, xin, yout, n, k):
+                if prepacked:
+                    w4.gemv_prepacked(m[0], xin, n, k, M, y=yout)
+                else:
+                    w4.gemv(m[0], m[1], xin, n, k, M, y=yout)
+            lin(d, act_ref, h_ref, K, N)
+            w4.swiglu(g[0], g[1], u[0], u[1], h_ref, N, K, M, y=act2_ref, prepacked=prepacked)
+            lin(d, act2_ref, h2_ref, K, N)
+        torch.cuda.synchronize()
+
+        act = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+        h = torch.full((M, K), float("nan"), dtype=torch.bfloat16, device=dev)
+        h2 = torch.full((M, K), float("nan"), dtype=torch.bfloat16, device=dev)
+        pw = lambda m: (m[0].data_ptr(), None if m[1] is None else m[1].data_ptr())  # noqa: E731
+        gu = [(*pw(g), 0, N), (*pw(u), 0, N)]
+        stages = [(gu, xk, K, -1, act)]
+        if down:
+            stages += [([(*pw(d), h.data_ptr(), K)], act, N, 0),
+                       (gu, h, K, 1, act),
+                       ([(*pw(d), h2.data_ptr(), K)], act, N, 2)]
+        chain = w4.Chain(stages, M, prepacked=prepacked)
+        for rep in range(2):
+            chain.run()
+            chain.status()
+            if down:
+                assert np.array_equal(_bits(h), _bits(h_ref)), (b, rep, "h")
+                assert np.array_equal(_bits(h2), _bits(h2_ref)), (b, rep, "h2")
+                assert np.array_equal(_bits(act), _bits(act2_ref)), (b, rep, "act")
+            else:
+                assert np.array_equal(_bits(act).ravel(), _bits(act_ref).ravel()), (b, rep, "act")
+            act.fill_(float("nan"))
+            h.fill_(float("nan"))
+            h2.fill_(float("nan"))
+
+
+def test_chain_swiglu_infinite_and_errors(orc, w4, dev):
+    """An infinity in x reaches both projections of a SwiGLU stage (their
+    NaN sums take the reference loop): act equals cudalm_w4a16_swiglu_bf16's
+    bits. The plan rejects SwiGLU stages that are not gate/up pairs of one
+    shape at K <= 2048."""
+    N, K, M = 1024, 1024, 4
+    g = _dev_mat(orc, w4, dev, 0xC4A1D000, N, K, True)
+    u = _dev_mat(orc, w4, dev, 0xC4A1D001, N, K, True)
+    X = orc.synth_act(0xC4A1D002, M, K)
+    X[1, 5] = 0x7F80  # +Inf
+    x = torch.from_numpy(X.view(np.int16)).to(dev).view(torch.bfloat16)
+    act = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    gu = [(g[0].data_ptr(), None, 0, N), (u[0].data_ptr(), None, 0, N)]
+    chain = w4.Chain([(gu, x, K, -1, act)], M, prepacked=True)
+    chain.run()
+    chain.status()
+    ref = w4.swiglu(g[0], None, u[0], None, x, N, K, M, prepacked=True)
+    assert np.array_equal(_bits(act).ravel(), _bits(ref).ravel())
+    assert not np.isfinite(orc.bf16_to_f32(_bits(act).reshape(M, N)[1])).all()
+
+    with pytest.raises(ValueError):  # one projection
+        w4.Chain([(gu[:1], x, K, -1, act)], M, prepacked=True)
+    with pytest.raises(ValueError):  # gate and up of different N
+        w4.Chain([([gu[0], (u[0].data_ptr(), None, 0, N - 16)], x, K, -1, act)], M, prepacked=True)
+    big = torch.zeros((M, 4096), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):  # K > 2048
+        w4.Chain([(gu, big, 4096, -1, act)], M, prepacked=True)
