@@ -157,9 +157,9 @@ struct StageProj {
   int begin;  // first stage tile of the projection
 };
 
-__device__ __forceinline__ StageProj stage_proj(const ChainStage& S, int t) {
+__device__ __forceinline__ StageProj stage_proj(const ChainStage& S, int t, bool epi) {
   StageProj v = {S.w[0], S.s[0], S.y[0], S.n[0], 0};
-  if (S.act != nullptr) {
+  if (epi) {
     if (t & 1) {
       v.w = S.w[1];
       v.s = S.s[1];
@@ -233,12 +233,19 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
                                             uint32_t* err, uint32_t ticks) {
   using Park = typename std::conditional<NR == 1, float, f32x4_t>::type;
   constexpr int kChainFrag = chain_frag(GPW, CT);
-  const int lane = threadIdx.x & 63;
+  // At two column tiles the lane index is made opaque per stage: otherwise
+  // the compiler hoists every lane-derived address and row mask of every
+  // stage path out of the stage loop, and those spill to scratch (with one
+  // column tile the hoisted values fit, and hoisting them is faster).
+  int tid = static_cast<int>(threadIdx.x);
+  if constexpr (CT == 2) asm volatile("" : "+v"(tid));
+  const int lane = tid & 63;
   const int wave = wave_id();
   const int i = lane & 15, a = lane >> 4;
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
   const int K = S.K;
   const int G = K >> 7;
+  const bool epi = S.act != nullptr;  // read once, before the wait
   constexpr int gpw = GPW;
   const int tpw = S.tpw;
   const int ntl = S.ntiles;
@@ -248,7 +255,11 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
   uint32_t* xch = reinterpret_cast<uint32_t*>(scs + static_cast<size_t>(gt_max) * 16);
   // this wave's activation fragments and offset chains, per owned group
   u32x4_t xa[GPW][CT][4];
-  f32x4_t off[GPW][CT];
+  // The offset chains are kept for the round's tiles, except where one tile
+  // per round uses each once and the registers are short (four groups per
+  // wave, two column tiles): there they are built where they are used.
+  constexpr bool KEEP_OFF = !(GPW == 4 && CT == 2);
+  f32x4_t off[KEEP_OFF ? GPW : 1][CT];
   bool have_x = false;
   for (int c = slot; c * tpw < ntl; c += S.nwg) {
     const int t0 = c * tpw;
@@ -262,7 +273,7 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
       const int g = wave + kChainWaves * q;
       if (j < tn && g < G) {
         const int t = t0 + j;
-        const StageProj v = stage_proj(S, t);
+        const StageProj v = stage_proj(S, t, epi);
         const int rt = t - v.begin;
         if constexpr (PACKED) {
           const uint8_t* tile = v.w + static_cast<size_t>(rt) * packed_tile_bytes(G);
@@ -316,11 +327,12 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
           }
         }
       }
+      if constexpr (KEEP_OFF)
 #pragma unroll
-      for (int q = 0; q < GPW; ++q)
-        if (q < gpw && wave + kChainWaves * q < G)
+        for (int q = 0; q < GPW; ++q)
+          if (q < gpw && wave + kChainWaves * q < G)
 #pragma unroll
-          for (int ct = 0; ct < CT; ++ct) off[q][ct] = group_offset(xa[q][ct]);
+            for (int ct = 0; ct < CT; ++ct) off[q][ct] = group_offset(xa[q][ct]);
     }
     // group results of this round's fragments into the park area
 #pragma unroll
@@ -330,8 +342,10 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
       if (j < tn && g < G) {
         f32x4_t t[CT];
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-          t[ct] = NR == 1 ? f32x4_t{off[q][ct][0], 0.0f, 0.0f, 0.0f} : off[q][ct];
+        for (int ct = 0; ct < CT; ++ct) {
+          const f32x4_t o = KEEP_OFF ? off[KEEP_OFF ? q : 0][ct] : group_offset(xa[q][ct]);
+          t[ct] = NR == 1 ? f32x4_t{o[0], 0.0f, 0.0f, 0.0f} : o;
+        }
 #pragma unroll
         for (int d = 0; d < 4; ++d)
 #pragma unroll
@@ -351,10 +365,9 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
     __syncthreads();
     // tile t0 + wave: the canonical chain over the parked group results
     const int j = wave;
-    f32x4_t total[CT];
+    auto tile_total = [&](f32x4_t (&total)[CT]) {
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
-    if (wave < tn) {
+      for (int ct = 0; ct < CT; ++ct) total[ct] = zero;
       for (int u = 0; u < U; ++u) {
         f32x4_t p[CT];
 #pragma unroll
@@ -377,23 +390,47 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) total[ct] = total[ct] + p[ct];
       }
-    }
-    const int t = t0 + j;
-    const StageProj v = stage_proj(S, t);
-    const int Nj = v.n;
-    const int n = (t - v.begin) * kTileRows + i;
-    // y bits of (ct, r) for this lane's column n; a NaN sum (infinite or NaN
-    // activations, overflow) is recomputed by the reference loop, keeping
-    // its semantics
-    auto out_bits = [&](int ct, int r, int m) -> uint32_t {
-      float val = 16.0f * total[ct][r];
+    };
+    // y bits of output row m, column n of projection v; a NaN sum (infinite
+    // or NaN activations, overflow) is recomputed by the reference loop,
+    // keeping its semantics
+    auto out_bits = [&](float sum, const StageProj& v, int n, int m) -> uint32_t {
+      float val = 16.0f * sum;
       if (__builtin_expect(val != val, 0))
         val = w4a16_ref_dot<PACKED, false, true>(v.w, v.s, K, n, S.x + static_cast<size_t>(m) * K);
       return f32_to_bf16_rne(val);
     };
-    if (S.act != nullptr) {
-      // SwiGLU: the up wave of each pair parks its bf16 outputs, then the
-      // gate wave writes act = silu(gate) * up
+    if (!epi) {
+      if (wave < tn) {
+        f32x4_t total[CT];
+        tile_total(total);
+        const int t = t0 + j;
+        const StageProj v = stage_proj(S, t, epi);
+        const int Nj = v.n;
+        const int n = (t - v.begin) * kTileRows + i;
+        if (n < Nj) {
+          uint16_t* col = v.y + n;
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+              const int m = ct * 16 + 4 * a + r;
+              if (m < M)
+                st_dev_u16(col + static_cast<size_t>(m) * Nj,
+                           static_cast<uint16_t>(out_bits(total[ct][r], v, n, m)));
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
+      }
+    } else {
+      // SwiGLU: the up wave (odd j) of each pair parks its bf16 outputs, then
+      // the gate wave writes act = silu(gate) * up
+      f32x4_t total[CT];
+      if (wave < tn) tile_total(total);
+      const int t = t0 + j;
+      const StageProj v = stage_proj(S, t, epi);
+      const int Nj = v.n;
+      const int n = (t - v.begin) * kTileRows + i;
       uint32_t* px = xch + static_cast<size_t>(j >> 1) * CT * NR * 64;
       if (wave < tn && (j & 1) && n < Nj) {
 #pragma unroll
@@ -401,7 +438,7 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
 #pragma unroll
           for (int r = 0; r < NR; ++r) {
             const int m = ct * 16 + 4 * a + r;
-            if (m < M) px[(ct * NR + r) * 64 + lane] = out_bits(ct, r, m);
+            if (m < M) px[(ct * NR + r) * 64 + lane] = out_bits(total[ct][r], v, n, m);
           }
       }
       __syncthreads();
@@ -414,20 +451,12 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
             const int m = ct * 16 + 4 * a + r;
             if (m < M)
               st_dev_u16(col + static_cast<size_t>(m) * Nj,
-                         static_cast<uint16_t>(silu_mul_bits(out_bits(ct, r, m), px[(ct * NR + r) * 64 + lane])));
+                         static_cast<uint16_t>(silu_mul_bits(out_bits(total[ct][r], v, n, m),
+                                                             px[(ct * NR + r) * 64 + lane])));
           }
       }
-    } else if (wave < tn && n < Nj) {
-      uint16_t* col = v.y + n;
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          const int m = ct * 16 + 4 * a + r;
-          if (m < M) st_dev_u16(col + static_cast<size_t>(m) * Nj, static_cast<uint16_t>(out_bits(ct, r, m)));
-        }
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
     __syncthreads();  // every store of the round is complete; the park area is free
   }
 }
