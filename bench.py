@@ -493,15 +493,28 @@ def main():
                         "source": PROFILE_CENSUS})
             # stage chain: the fused groups as dependent stages of one
             # persistent launch (each waits for the previous one, the
-            # runtime's worst case), then the LM head launch
-            for key in (f"M{Mc}_chain",):
+            # runtime's worst case), then the LM head launch. The _swiglu
+            # form runs every MLP as the reference's data flow: gate/up as a
+            # SwiGLU stage writing act = silu(gate) * up (the
+            # qwen35_silu_mul_bf16 step, with no launch of its own), down
+            # reading act.
+            act = torch.empty((Mc, MLP[0][1]), dtype=torch.bfloat16, device=dev)
+            for key in (f"M{Mc}_chain", f"M{Mc}_chain_swiglu"):
                 if args.census_mode and args.census_mode != key:
                     continue
+                swiglu = key.endswith("_swiglu")
                 stages = []
                 for gi, group in enumerate(census_groups(True)):
                     Kc = group[0][3]
+                    names = [nm for _, nm, _, _ in group]
+                    xin = xs[Kc].data_ptr()
+                    extra = ()
+                    if swiglu and names == ["gate_proj", "up_proj"]:
+                        extra = (act,)
+                    elif swiglu and names == ["down_proj"]:
+                        xin = act.data_ptr()
                     stages.append(([(cw[(li, nm)].data_ptr(), None, ys[(li, nm)].data_ptr(), Nc)
-                                    for li, nm, Nc, _ in group], xs[Kc].data_ptr(), Kc, gi - 1))
+                                    for li, nm, Nc, _ in group], xin, Kc, gi - 1) + extra)
                 chain = w4.Chain(stages, Mc, prepacked=True, stream=stream)
                 hp, xhp, yhp = packs[0].data_ptr(), xh.data_ptr(), yh.data_ptr()
 
@@ -519,6 +532,7 @@ def main():
                     "us_per_decode_step": round(t * 1e6, 2),
                     "launches": 2,
                     "stages": len(stages),
+                    **({"swiglu_stages": sum(len(sg) == 5 for sg in stages)} if swiglu else {}),
                     "bytes": tot_bytes,
                     "GBps": round(tot_bytes / t / 1e9, 1),
                     "frac_hbm_peak": round(tot_bytes / t / 1e9 / HBM_PEAK_GBS, 4),

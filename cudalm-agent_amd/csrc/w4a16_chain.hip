@@ -423,8 +423,9 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
         __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
       }
     } else {
-      // SwiGLU: the up wave (odd j) of each pair parks its bf16 outputs, then
-      // the gate wave writes act = silu(gate) * up
+      // SwiGLU: the up wave (odd j) of each pair parks its bf16 outputs
+      // while the gate wave (even j) rounds silu(g); then the gate wave
+      // writes act = silu(g) * up
       f32x4_t total[CT];
       if (wave < tn) tile_total(total);
       const int t = t0 + j;
@@ -432,13 +433,20 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
       const int Nj = v.n;
       const int n = (t - v.begin) * kTileRows + i;
       uint32_t* px = xch + static_cast<size_t>(j >> 1) * CT * NR * 64;
-      if (wave < tn && (j & 1) && n < Nj) {
+      uint32_t sb[CT][NR];
+      if (wave < tn && n < Nj) {
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
           for (int r = 0; r < NR; ++r) {
             const int m = ct * 16 + 4 * a + r;
-            if (m < M) px[(ct * NR + r) * 64 + lane] = out_bits(total[ct][r], v, n, m);
+            if (m < M) {
+              const uint32_t o = out_bits(total[ct][r], v, n, m);
+              if (j & 1)
+                px[(ct * NR + r) * 64 + lane] = o;
+              else
+                sb[ct][r] = silu_bits(o);
+            }
           }
       }
       __syncthreads();
@@ -451,8 +459,7 @@ __device__ __forceinline__ void chain_stage(const ChainStage& S, int slot, int M
             const int m = ct * 16 + 4 * a + r;
             if (m < M)
               st_dev_u16(col + static_cast<size_t>(m) * Nj,
-                         static_cast<uint16_t>(silu_mul_bits(out_bits(total[ct][r], v, n, m),
-                                                             px[(ct * NR + r) * 64 + lane])));
+                         static_cast<uint16_t>(mul_bits(sb[ct][r], px[(ct * NR + r) * 64 + lane])));
           }
       }
       __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete

@@ -129,10 +129,17 @@ __device__ __forceinline__ float w4a16_ref_dot(const uint8_t* W, const uint16_t*
 // y = bf16( f32(bf16(g / (1 + exp(-g)))) * u ) on bf16 inputs g, u: SiLU in
 // fp32, rounded to bf16 first, then the product rounded once
 // (include/cudalm/kernels/qwen35_kernels.h:146-152).
-__device__ __forceinline__ uint32_t silu_mul_bits(uint32_t g_bits, uint32_t u_bits) {
+// silu_mul_bits(g, u) == mul_bits(silu_bits(g), u): the two roundings as
+// separate steps, for callers that have g before u.
+__device__ __forceinline__ uint32_t silu_bits(uint32_t g_bits) {
   const float g = bf16_lo(g_bits);
-  const float s = bf16_lo(f32_to_bf16_rne(g / (1.0f + expf(-g))));
-  return f32_to_bf16_rne(s * bf16_lo(u_bits));
+  return f32_to_bf16_rne(g / (1.0f + expf(-g)));
+}
+__device__ __forceinline__ uint32_t mul_bits(uint32_t s_bits, uint32_t u_bits) {
+  return f32_to_bf16_rne(bf16_lo(s_bits) * bf16_lo(u_bits));
+}
+__device__ __forceinline__ uint32_t silu_mul_bits(uint32_t g_bits, uint32_t u_bits) {
+  return mul_bits(silu_bits(g_bits), u_bits);
 }
 
 // Prefill-chunk GEMM on 32 x 32 MFMA tiles (w4a16_gemm.hip): 32 activation
