@@ -508,13 +508,13 @@ def main():
                     Kc = group[0][3]
                     names = [nm for _, nm, _, _ in group]
                     xin = xs[Kc].data_ptr()
-                    extra = ()
+                    act_arg = ()
                     if swiglu and names == ["gate_proj", "up_proj"]:
-                        extra = (act,)
+                        act_arg = (act,)
                     elif swiglu and names == ["down_proj"]:
                         xin = act.data_ptr()
                     stages.append(([(cw[(li, nm)].data_ptr(), None, ys[(li, nm)].data_ptr(), Nc)
-                                    for li, nm, Nc, _ in group], xin, Kc, gi - 1) + extra)
+                                    for li, nm, Nc, _ in group], xin, Kc, gi - 1) + act_arg)
                 chain = w4.Chain(stages, Mc, prepacked=True, stream=stream)
                 hp, xhp, yhp = packs[0].data_ptr(), xh.data_ptr(), yh.data_ptr()
 

@@ -145,9 +145,22 @@ def test_cpp_headers_compile_and_link(tmp_path, w4):
 #include "cudalm_bf16_gemv.h"
 #include "cudalm_v2.h"
 #include "cudalm_w4a16.h"
+#include <cstddef>
 #include <cstdio>
 int main() {
   std::printf("%zu %zu\n", cudalm::packed_w4a16_bytes(16, 128), cudalm_w4a16_packed_bytes(32, 256));
+  // struct layouts the Python layer mirrors with ctypes
+  std::printf("stage %zu %zu %zu %zu %zu %zu %zu\n", sizeof(cudalm_w4a16_stage),
+              offsetof(cudalm_w4a16_stage, projs), offsetof(cudalm_w4a16_stage, count),
+              offsetof(cudalm_w4a16_stage, x), offsetof(cudalm_w4a16_stage, K),
+              offsetof(cudalm_w4a16_stage, dep), offsetof(cudalm_w4a16_stage, act));
+  std::printf("proj %zu %zu %zu %zu %zu\n", sizeof(cudalm_w4a16_proj),
+              offsetof(cudalm_w4a16_proj, weight), offsetof(cudalm_w4a16_proj, scale),
+              offsetof(cudalm_w4a16_proj, y), offsetof(cudalm_w4a16_proj, N));
+  std::printf("chain %zu %zu %zu %zu %zu %zu %zu\n", sizeof(cudalm_w4a16_chain),
+              offsetof(cudalm_w4a16_chain, workspace), offsetof(cudalm_w4a16_chain, n_stages),
+              offsetof(cudalm_w4a16_chain, M), offsetof(cudalm_w4a16_chain, prepacked),
+              offsetof(cudalm_w4a16_chain, grid), offsetof(cudalm_w4a16_chain, gt_max));
   // the reference-named bf16 entry points resolve at link time
   void (*f1)(const __hip_bfloat16*, const __hip_bfloat16*, __hip_bfloat16*, int, int, hipStream_t) =
       cudalm::bf16_gemv;
@@ -168,7 +181,13 @@ int main() {
     assert res.returncode == 0, res.stderr
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stderr
-    assert out.stdout.split() == ["1280", str(2 * (2 * 1024 + 256))]
+    lines = out.stdout.splitlines()
+    assert lines[0].split() == ["1280", str(2 * (2 * 1024 + 256))]
+    for line in lines[1:]:
+        name, *nums = line.split()
+        cls = {"stage": w4.Stage, "proj": w4.Proj, "chain": w4.ChainHandle}[name]
+        want = [ctypes.sizeof(cls)] + [getattr(cls, f).offset for f, _ in cls._fields_]
+        assert [int(v) for v in nums] == want, (name, nums, want)
 
 
 def test_cpp_entry_aborts_on_precondition(tmp_path, w4):
