@@ -53,6 +53,11 @@ struct Bf16Unit {
 // layout just before its steps. Rows are kStagePitch bytes apart (128 B of
 // data + 16 B) so the 16 rows' operand reads spread over the LDS banks.
 // Measured on the LM head (N = 248320, K = 1024, M = 1): 88.4 -> 79.2 us.
+// Read-only target of a wave's last, unused unit load (both layouts):
+// one unit (8 slabs of 1 KB), never written. The loop's loads stay
+// unconditional without re-reading a non-temporally loaded unit from HBM.
+__device__ __align__(256) uint16_t g_bf16_unit_sink[kSteps * 512];
+
 constexpr int kStagePitch = 144;
 constexpr int kStageBytes = kTile * kStagePitch;  // per wave
 
@@ -60,13 +65,15 @@ constexpr int kStageBytes = kTile * kStagePitch;  // per wave
 // are zeroed at use, so a partial last unit or tile needs no branch around
 // the loads.
 __device__ __forceinline__ void bf16_unit_load(Bf16Unit& v, const uint16_t* __restrict__ W, int N,
-                                               int K, int tile, int u, int lane) {
+                                               int K, int tile, int u, int lane, bool real) {
   const int r = lane >> 3, c = lane & 7;
 #pragma unroll
   for (int q = 0; q < kSteps; ++q) {
-    const uint16_t* wrow = W + static_cast<size_t>(min(tile * kTile + 8 * (q & 1) + r, N - 1)) * K;
-    v.w[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(
-        wrow + min(u * kUnitK + 64 * (q >> 1) + 8 * c, K - 8)));
+    const uint16_t* p =
+        real ? W + static_cast<size_t>(min(tile * kTile + 8 * (q & 1) + r, N - 1)) * K +
+                   min(u * kUnitK + 64 * (q >> 1) + 8 * c, K - 8)
+             : g_bf16_unit_sink + q * 512 + lane * 8;
+    v.w[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
   }
 }
 
@@ -80,10 +87,6 @@ __device__ __forceinline__ void wave_lds_sync() {
 // consecutive 1 KB slabs, slab j holding, at byte 16 l, lane l's 16 bytes of
 // MFMA step j (row 16 t + l % 16, k = 256 u + 32 j + 8 (l / 16)), so every
 // wave-wide load reads 1 KB contiguous. Requires N % 16 == 0, K % 256 == 0.
-// Read-only target of a wave's last, unused unit load on the packed copy:
-// one unit (8 slabs of 1 KB), never written. The loop's loads stay
-// unconditional without re-reading a non-temporally loaded unit from HBM.
-__device__ __align__(256) uint16_t g_bf16_unit_sink[kSteps * 512];
 
 __device__ __forceinline__ void bf16_unit_load_packed(Bf16Unit& v, const uint16_t* __restrict__ Wp,
                                                       int U, int tile, int u, int lane, bool real) {
@@ -149,7 +152,7 @@ __global__ __launch_bounds__(kWaves * 64) void bf16_gemv_stream_kernel(
   if constexpr (PACKED)
     bf16_unit_load_packed(cur, W, U, min(t, ntiles - 1), 0, lane, true);
   else
-    bf16_unit_load(cur, W, N, K, min(t, ntiles - 1), 0, lane);
+    bf16_unit_load(cur, W, N, K, min(t, ntiles - 1), 0, lane, true);
   const int nb = U * (kUnitK / 8);
   for (int e = threadIdx.x; e < mrows * nb; e += blockDim.x) {
     const int mm = e / nb;
@@ -180,12 +183,12 @@ __global__ __launch_bounds__(kWaves * 64) void bf16_gemv_stream_kernel(
       nt = t + stride;
     }
     const bool has_next = nt < ntiles;
-    // past the last unit, re-read the current one (cache hits) instead of
-    // branching around the loads
+    // past the last unit, read the sink unit instead of branching around
+    // the loads
     if constexpr (PACKED)
       bf16_unit_load_packed(nxt, W, U, nt, nu, lane, has_next);
     else
-      bf16_unit_load(nxt, W, N, K, has_next ? nt : t, has_next ? nu : u, lane);
+      bf16_unit_load(nxt, W, N, K, nt, nu, lane, has_next);
     bf16_unit_mma<CT, !PACKED>(acc, cur, xrow, u, K, lane, stage);
     if (u == U - 1) {
       const int n = t * kTile + i;
