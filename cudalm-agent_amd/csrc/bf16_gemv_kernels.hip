@@ -77,11 +77,6 @@ __device__ __forceinline__ void bf16_unit_load(Bf16Unit& v, const uint16_t* __re
   }
 }
 
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Tile-major layout (cudalm_bf16_repack): the unit u of tile t is 8
 // consecutive 1 KB slabs, slab j holding, at byte 16 l, lane l's 16 bytes of

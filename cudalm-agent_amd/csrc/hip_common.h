@@ -22,6 +22,15 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr size_t kLdsMax = 160 * 1024;  // LDS per CU (and per workgroup) on gfx950
 
 // Wave index inside the workgroup, as a wave-uniform (scalar) value.
+// Orders one wave's LDS writes before its later LDS reads (and those reads
+// before later writes) when lanes exchange data through LDS: the LDS unit
+// serves a wave's operations in order, so only the compiler needs fencing.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
 }

@@ -617,19 +617,10 @@ __device__ __forceinline__ TileAddr tile_addr(const PT& P, int K, int G, int t, 
   }
 }
 
-// FULL: G is a multiple of HG, so no group index needs clamping.
-template <int HG, bool PACKED, bool SVEC, bool FULL>
-__device__ __forceinline__ void stream_load_piece(StreamPiece<HG>& h, TileAddr ad, int G, int g0) {
-  static_assert(HG == 1 || HG == 2 || HG == 4, "piece of 1, 2 or 4 groups");
-  // a piece past a wave's last one is read from g_piece_sink: it must fit
-  static_assert(HG * 1024 + 64 * 16 <= sizeof(g_piece_sink), "the sink must hold a whole piece");
-  constexpr int kStep = PACKED ? 1024 : 64;  // bytes between groups of one lane
-  const uint8_t* wp = ad.w + static_cast<size_t>(g0) * kStep;
-#pragma unroll
-  for (int gg = 0; gg < HG; ++gg) {
-    const int off = FULL ? gg : min(g0 + gg, G - 1) - g0;
-    h.w[gg] = load_weights(wp + off * kStep);
-  }
+// The fp16 scales of a piece for this lane's weight row (ad.s: the row's
+// scales at group 0).
+template <int HG, bool PACKED, bool SVEC>
+__device__ __forceinline__ void stream_load_scales(StreamPiece<HG>& h, TileAddr ad, int G, int g0) {
   if constexpr (PACKED || SVEC) {
     // packed scale rows are 16 B aligned; SVEC file rows too (G % 8 == 0)
     if constexpr (HG == 4) {
@@ -650,6 +641,83 @@ __device__ __forceinline__ void stream_load_piece(StreamPiece<HG>& h, TileAddr a
     for (int q = 0; q < HG / 2; ++q) h.s[q] = v[2 * q] | (v[2 * q + 1] << 16);
     if constexpr (HG == 1) h.s[0] = v[0];
   }
+}
+
+// FULL: G is a multiple of HG, so no group index needs clamping.
+template <int HG, bool PACKED, bool SVEC, bool FULL>
+__device__ __forceinline__ void stream_load_piece(StreamPiece<HG>& h, TileAddr ad, int G, int g0) {
+  static_assert(HG == 1 || HG == 2 || HG == 4, "piece of 1, 2 or 4 groups");
+  // a piece past a wave's last one is read from g_piece_sink: it must fit
+  static_assert(HG * 1024 + 64 * 16 <= sizeof(g_piece_sink), "the sink must hold a whole piece");
+  constexpr int kStep = PACKED ? 1024 : 64;  // bytes between groups of one lane
+  const uint8_t* wp = ad.w + static_cast<size_t>(g0) * kStep;
+#pragma unroll
+  for (int gg = 0; gg < HG; ++gg) {
+    const int off = FULL ? gg : min(g0 + gg, G - 1) - g0;
+    h.w[gg] = load_weights(wp + off * kStep);
+  }
+  stream_load_scales<HG, PACKED, SVEC>(h, ad, G, g0);
+}
+
+// File-layout pieces of 4 groups in whole lines. In the lane layout the
+// MFMA operand needs (row 16 rt + i, 16 bytes at 64 g + 16 a), every wave
+// load reads 64 B from each of 16 rows; here load q reads rows
+// 16 rt + 4 q .. +3, 256 contiguous bytes each (the piece's 4 groups; lane
+// l: row 4 q + l / 16, byte 16 (l % 16) of the piece), and the step re-lays
+// the piece out through the wave's LDS staging rows (coal_relayout). Rows
+// past the matrix are clamped to its last row, as in tile_addr.
+struct CoalAddr {
+  const uint8_t* w;  // row 16 rt + lane / 16 (clamped) at group 0
+  uint32_t d[3];     // bytes from w to rows +4, +8, +12 (clamped)
+  const uint8_t* s;  // this lane's scale row (row 16 rt + lane % 16), as tile_addr
+};
+
+constexpr int kCoalPitch = 272;                       // bytes per staged row: 256 + 16
+constexpr int kCoalStageBytes = kTileRows * kCoalPitch;  // per wave
+
+template <class PT>
+__device__ __forceinline__ CoalAddr coal_addr(const PT& P, int K, int G, int t, int lane) {
+  const ProjView v = proj_view(P, t);
+  const int rt = t - v.begin;
+  const int r0 = rt * kTileRows + (lane >> 4);
+  const int rb = min(r0, v.n - 1);
+  const uint32_t rowb = static_cast<uint32_t>(K >> 1);
+  CoalAddr c;
+  c.w = v.w + static_cast<size_t>(rb) * rowb;
+#pragma unroll
+  for (int q = 1; q < 4; ++q) c.d[q - 1] = static_cast<uint32_t>(min(r0 + 4 * q, v.n - 1) - rb) * rowb;
+  const int row = min(rt * kTileRows + (lane & 15), v.n - 1);
+  c.s = reinterpret_cast<const uint8_t*>(v.s + static_cast<size_t>(row) * G);
+  return c;
+}
+
+template <bool SVEC, bool FULL>
+__device__ __forceinline__ void coal_load_piece(StreamPiece<4>& h, const CoalAddr& ad, int G, int g0,
+                                                int lane) {
+  const int c = lane & 15;
+  const uint32_t off = FULL ? static_cast<uint32_t>(g0 * 64 + 16 * c)
+                            : static_cast<uint32_t>(min(g0 + (c >> 2), G - 1) * 64 + 16 * (c & 3));
+  h.w[0] = load_weights(ad.w + off);
+#pragma unroll
+  for (int q = 1; q < 4; ++q) h.w[q] = load_weights(ad.w + ad.d[q - 1] + off);
+  stream_load_scales<4, false, SVEC>(h, TileAddr{ad.w, ad.s}, G, g0);
+}
+
+// The loaded piece (coalesced layout) into the lane layout, through this
+// wave's staging rows.
+__device__ __forceinline__ void coal_relayout(StreamPiece<4>& out, const StreamPiece<4>& in,
+                                              uint8_t* stage, int lane) {
+  const int i = lane & 15, a = lane >> 4;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<u32x4_t*>(stage + (4 * q + (lane >> 4)) * kCoalPitch + 16 * (lane & 15)) = in.w[q];
+  wave_lds_sync();
+#pragma unroll
+  for (int gg = 0; gg < 4; ++gg)
+    out.w[gg] = *reinterpret_cast<const u32x4_t*>(stage + i * kCoalPitch + 64 * gg + 16 * a);
+  wave_lds_sync();  // read before the next piece overwrites the rows
+#pragma unroll
+  for (int q = 0; q < 2; ++q) out.s[q] = in.s[q];
 }
 
 template <int HG, int NR, int CT, class Act, bool FULL, bool IOFF = false>
@@ -686,12 +754,31 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
   int t = persistent ? blockIdx.x * WV + wave : t_static + (blockIdx.x - pwg) * WV + wave;
   const bool active = t < ntiles;
 
+  // File-layout weights of one column tile are loaded in whole lines and
+  // re-laid out through per-wave LDS staging rows after the offset table.
+  constexpr bool COAL = !PACKED && HG == 4 && CT == 1;
+  using Addr = typename std::conditional<COAL, CoalAddr, TileAddr>::type;
+  auto addr_of = [&](int tt) -> Addr {
+    if constexpr (COAL)
+      return coal_addr(P, K, G, tt, lane);
+    else
+      return tile_addr<PACKED>(P, K, G, tt, lane);
+  };
+  auto load_piece = [&](StreamPiece<HG>& b, const Addr& ad, int g0) {
+    if constexpr (COAL)
+      coal_load_piece<SVEC, FULL>(b, ad, G, g0, lane);
+    else
+      stream_load_piece<HG, PACKED, SVEC, FULL>(b, ad, G, g0);
+  };
+  uint8_t* stage = reinterpret_cast<uint8_t*>(xs) + static_cast<size_t>(M) * x_pitch(K) * 16 +
+                   static_cast<size_t>(G) * 64 * CT + wave * kCoalStageBytes;
+
   // x's first batch, then the first piece's weights, fly together
   StageBatch sb0;
   stage_load(sb0, X, K, 0, M, 0, K, 0);
   StreamPiece<HG> bufA, bufB;
-  TileAddr acur = tile_addr<PACKED>(P, K, G, min(t, ntiles - 1), lane);
-  stream_load_piece<HG, PACKED, SVEC, FULL>(bufA, acur, G, 0);
+  Addr acur = addr_of(min(t, ntiles - 1));
+  load_piece(bufA, acur, 0);
   const u32x4_t* xrow[CT];
   const float* corr = stream_prologue<CT, Act, IOFF>(xs, xrow, X, K, M, wave, i, a, sb0);
   if (!active) return;
@@ -723,15 +810,25 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
       nt = t + stride;
     }
     const bool has_next = nt < ntiles;
-    TileAddr anx = acur;
-    if (has_next && nh == 0) anx = tile_addr<PACKED>(P, K, G, nt, lane);
+    Addr anx = acur;
+    if (has_next && nh == 0) anx = addr_of(nt);
     // past the last piece, load from the sink instead of branching around
     // the loads (the scales re-read the current tile's, cached)
-    if (!has_next) anx.w = g_piece_sink + lane * 16;
-    stream_load_piece<HG, PACKED, SVEC, FULL>(nxt, anx, G, (has_next ? nh : 0) * HG);
+    if (!has_next) {
+      anx.w = g_piece_sink + lane * 16;
+      if constexpr (COAL) anx.d[0] = anx.d[1] = anx.d[2] = 0;
+    }
+    load_piece(nxt, anx, (has_next ? nh : 0) * HG);
     const int g0 = h * HG;
-    stream_piece<HG, NR, CT, Layout<Act, PACKED>, FULL, IOFF>(part, cur, xrow, corr, g0,
-                                                             min(HG, G - g0), a);
+    if constexpr (COAL) {
+      StreamPiece<HG> lay;
+      coal_relayout(lay, cur, stage, lane);
+      stream_piece<HG, NR, CT, Layout<Act, PACKED>, FULL, IOFF>(part, lay, xrow, corr, g0,
+                                                               min(HG, G - g0), a);
+    } else {
+      stream_piece<HG, NR, CT, Layout<Act, PACKED>, FULL, IOFF>(part, cur, xrow, corr, g0,
+                                                               min(HG, G - g0), a);
+    }
     // an 8-group unit ends after its last piece or at the tile's last piece
     if ((h % PPU) == PPU - 1 || h == H - 1) {
 #pragma unroll
@@ -1627,7 +1724,11 @@ size_t stream_lds_bytes(int K, int M) {
   return static_cast<size_t>(M) * x_pitch(K) * 16 + static_cast<size_t>(K / kGroup) * 64 * CT;
 }
 
-bool stream_fits(int K, int M) { return M <= 32 && stream_lds_bytes(K, M) <= kLdsMax; }
+// Counts the file-layout staging rows at one column tile for either layout.
+bool stream_fits(int K, int M) {
+  return M <= 32 &&
+         stream_lds_bytes(K, M) + (M <= 16 ? kStreamWaves * kCoalStageBytes : 0) <= kLdsMax;
+}
 
 int split_tiles_per_round(int K) {
   const int U = (K / kGroup + kUnit - 1) / kUnit;
@@ -1659,7 +1760,8 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   // most two workgroups fit a CU: 8-wave workgroups keep 16 waves resident
   // (measured 3.5 us faster than 4-wave ones on the M = 32 LM head).
   constexpr int WV = CT == 2 ? 8 : kStreamWaves;
-  const size_t lds = stream_lds_bytes(K, M);
+  // file-layout weights at one column tile: the staging rows after the table
+  const size_t lds = stream_lds_bytes(K, M) + (!PACKED && CT == 1 ? WV * kCoalStageBytes : 0);
   const int ntiles = P.ntiles;
   int per_cu = CT == 2 ? kStreamWideWgsPerCu : kStreamWgsPerCu;
   const int lds_fit = static_cast<int>(kLdsMax / (lds > 0 ? lds : 1));
