@@ -1724,10 +1724,16 @@ size_t stream_lds_bytes(int K, int M) {
   return static_cast<size_t>(M) * x_pitch(K) * 16 + static_cast<size_t>(K / kGroup) * 64 * CT;
 }
 
-// Counts the file-layout staging rows at one column tile for either layout.
-bool stream_fits(int K, int M) {
-  return M <= 32 &&
-         stream_lds_bytes(K, M) + (M <= 16 ? kStreamWaves * kCoalStageBytes : 0) <= kLdsMax;
+// LDS of the stream kernel: x and the offset table, plus the file-layout
+// staging rows at one column tile.
+size_t stream_kernel_lds(int K, int M, bool packed) {
+  const int WV = M > 16 ? 8 : kStreamWaves;
+  return stream_lds_bytes(K, M) +
+         (!packed && M <= 16 ? static_cast<size_t>(WV) * kCoalStageBytes : 0);
+}
+
+bool stream_fits(int K, int M, bool packed) {
+  return M <= 32 && stream_kernel_lds(K, M, packed) <= kLdsMax;
 }
 
 int split_tiles_per_round(int K) {
@@ -1761,7 +1767,7 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   // (measured 3.5 us faster than 4-wave ones on the M = 32 LM head).
   constexpr int WV = CT == 2 ? 8 : kStreamWaves;
   // file-layout weights at one column tile: the staging rows after the table
-  const size_t lds = stream_lds_bytes(K, M) + (!PACKED && CT == 1 ? WV * kCoalStageBytes : 0);
+  const size_t lds = stream_kernel_lds(K, M, PACKED);
   const int ntiles = P.ntiles;
   int per_cu = CT == 2 ? kStreamWideWgsPerCu : kStreamWgsPerCu;
   const int lds_fit = static_cast<int>(kLdsMax / (lds > 0 ? lds : 1));
@@ -2160,7 +2166,7 @@ template <bool PACKED>
 int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N, int K,
              int M, int variant, hipStream_t stream) {
   if (variant == CUDALM_W4A16_VARIANT_AUTO) {
-    if (stream_fits(K, M) || piece_direct((N + kTileRows - 1) / kTileRows, K, M)) {
+    if (stream_fits(K, M, PACKED) || piece_direct((N + kTileRows - 1) / kTileRows, K, M)) {
       const ProjTable P = single_table(W, S, Y, N);
       return launch_stream<PACKED>(P, X, K, M, stream);
     } else if (M <= 32 && M > 16) {
@@ -2181,7 +2187,7 @@ int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y
   }
   switch (variant) {
     case CUDALM_W4A16_VARIANT_STREAM:
-      if (!stream_fits(K, M)) return CUDALM_W4A16_EVARIANT;
+      if (!stream_fits(K, M, PACKED)) return CUDALM_W4A16_EVARIANT;
       return launch_stream_any<PACKED, false>(single_table(W, S, Y, N), X, K, M, stream);
     case CUDALM_W4A16_VARIANT_SPLIT:
       if (!split_fits(K, M) && split_piece_plan((N + kTileRows - 1) / kTileRows, K, M).hg == 0)
@@ -2211,7 +2217,7 @@ int f16_dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_
                  int K, int M, bool vec_ok, hipStream_t stream) {
   if (!vec_ok) return launch_bytewise<ActF16>(W, S, X, Y, N, K, M, stream);
   int mc = M < 32 ? M : 32;
-  while (mc > 0 && !stream_fits(K, mc)) --mc;
+  while (mc > 0 && !stream_fits(K, mc, PACKED)) --mc;
   if (mc < 1) return CUDALM_W4A16_ERANGE;
   for (int m0 = 0; m0 < M; m0 += mc) {
     const int rows = M - m0 < mc ? M - m0 : mc;
@@ -2321,7 +2327,7 @@ int cudalm_w4a16_gemv_bf16_multi(const cudalm_w4a16_proj* projs, int count, cons
   long long tiles = 0;
   for (int j = 0; j < count; ++j) tiles += (projs[j].N + kTileRows - 1) / kTileRows;
   if (!vec_ok || tiles > (1LL << 30) ||
-      (!stream_fits(K, M) && !piece_direct(static_cast<int>(tiles), K, M))) {
+      (!stream_fits(K, M, prepacked) && !piece_direct(static_cast<int>(tiles), K, M))) {
     // not one fused launch: one call per projection (same bits)
     for (int j = 0; j < count; ++j) {
       const int rc =
