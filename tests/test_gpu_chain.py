@@ -266,10 +266,13 @@ def test_chain_swiglu_mlp(orc, w4, dev, M, prepacked):
     output. Every output bit-identical to cudalm_w4a16_swiglu_bf16 followed
     by cudalm_w4a16_gemv_bf16, launch by launch. Shapes: the census MLP
     (3584 x 1024 gate/up), a ragged one at K = 2048 (two groups per wave,
-    1000 rows: 63 tile pairs) and a one-tile one."""
+    1000 rows: 63 tile pairs), a one-tile one and one that takes two rounds
+    (5000 x 2048)."""
     print(f"  chain swiglu M={M} prepacked={prepacked}", flush=True)
     seed = 0xC4A15000 + 31 * M + int(prepacked)
-    blocks = [(3584, 1024), (1000, 2048), (16, 1024)]  # (N of gate/up, K = hidden)
+    # (N of gate/up, K = hidden); 5000 x 2048 is 626 stage tiles at two per
+    # workgroup: more than one round of the 256 workgroups a stage may use
+    blocks = [(3584, 1024), (1000, 2048), (16, 1024), (5000, 2048)]
     mats = []
     for b, (N, K) in enumerate(blocks):
         g = _dev_mat(orc, w4, dev, seed + 8 * b, N, K, prepacked)
