@@ -332,6 +332,20 @@ struct StreamUnit {
   u32x4_t s;  // fp16 scales of the unit's 8 groups for this lane's weight row
 };
 
+// The fp16 scales of a unit's 8 groups from a file-layout scale row.
+template <bool SVEC>
+__device__ __forceinline__ void load_unit_scales(StreamUnit& u, const uint16_t* srow, int G, int g0) {
+  if constexpr (SVEC) {
+    u.s = *reinterpret_cast<const u32x4_t*>(srow + g0);
+  } else {
+    uint32_t h[kUnit];
+#pragma unroll
+    for (int gg = 0; gg < kUnit; ++gg) h[gg] = srow[min(g0 + gg, G - 1)];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) u.s[q] = h[2 * q] | (h[2 * q + 1] << 16);
+  }
+}
+
 // Loads are unconditional (group indices clamped to G-1) so the compiler's
 // memory counters see one straight-line batch per unit and the compute of
 // the current unit waits only for its own data.
@@ -353,17 +367,48 @@ __device__ __forceinline__ void stream_load(StreamUnit& u, const uint8_t* __rest
 #pragma unroll
     for (int gg = 0; gg < kUnit; ++gg)
       u.w[gg] = load_weights(wrow + min(g0 + gg, G - 1) * 64);
-    const uint16_t* srow = S + static_cast<size_t>(row) * G;
-    if constexpr (SVEC) {
-      u.s = *reinterpret_cast<const u32x4_t*>(srow + g0);
-    } else {
-      uint32_t h[kUnit];
-#pragma unroll
-      for (int gg = 0; gg < kUnit; ++gg) h[gg] = srow[min(g0 + gg, G - 1)];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) u.s[q] = h[2 * q] | (h[2 * q + 1] << 16);
-    }
+    load_unit_scales<SVEC>(u, S + static_cast<size_t>(row) * G, G, g0);
   }
+}
+
+// File-layout units in whole lines (the split kernel at one column tile):
+// load q reads rows 16 rt + 2 q and 2 q + 1, 512 contiguous bytes each (the
+// unit's 8 groups; lane l: row 2 q + l / 32, byte 16 (l % 32) of the unit)
+// instead of 64 B from each of 16 rows, and unit_relayout moves the unit
+// into the lane layout through the wave's LDS staging rows. Rows past the
+// matrix are clamped to its last row; scales as stream_load.
+constexpr int kUnitStagePitch = kUnit * 64 + 16;               // bytes per staged row
+constexpr int kUnitStageBytes = kTileRows * kUnitStagePitch;  // per wave
+
+template <bool SVEC, class PT>
+__device__ __forceinline__ void stream_load_coal_t(StreamUnit& u, const PT& P, int K, int G, int t,
+                                                   int g0, int lane) {
+  const ProjView v = proj_view(P, t);
+  const int rt = t - v.begin;
+  const int c = lane & 31;
+  const uint32_t off = static_cast<uint32_t>(min(g0 + (c >> 2), G - 1) * 64 + 16 * (c & 3));
+#pragma unroll
+  for (int q = 0; q < kUnit; ++q) {
+    const int rr = min(rt * kTileRows + 2 * q + (lane >> 5), v.n - 1);
+    u.w[q] = load_weights(v.w + static_cast<size_t>(rr) * (K >> 1) + off);
+  }
+  const int row = min(rt * kTileRows + (lane & 15), v.n - 1);
+  load_unit_scales<SVEC>(u, v.s + static_cast<size_t>(row) * G, G, g0);
+}
+
+__device__ __forceinline__ void unit_relayout(StreamUnit& out, const StreamUnit& in, uint8_t* stage,
+                                              int lane) {
+  const int i = lane & 15, a = lane >> 4;
+#pragma unroll
+  for (int q = 0; q < kUnit; ++q)
+    *reinterpret_cast<u32x4_t*>(stage + (2 * q + (lane >> 5)) * kUnitStagePitch + 16 * (lane & 31)) =
+        in.w[q];
+  wave_lds_sync();
+#pragma unroll
+  for (int gg = 0; gg < kUnit; ++gg)
+    out.w[gg] = *reinterpret_cast<const u32x4_t*>(stage + i * kUnitStagePitch + 64 * gg + 16 * a);
+  wave_lds_sync();  // read before the next unit overwrites the rows
+  out.s = in.s;
 }
 
 template <bool PACKED, bool SVEC, class PT>
@@ -884,28 +929,41 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
   // slot partials after the offset table: [nslots][CT][64 lanes] f32x4
   f32x4_t* slots = reinterpret_cast<f32x4_t*>(
       reinterpret_cast<float*>(xs + M * pitch) + G * 16 * CT);
+  // file-layout weights of one column tile: whole-line loads, re-laid out
+  // through per-wave staging rows after the slots
+  constexpr bool COAL = !PACKED && CT == 1;
+  uint8_t* stage = reinterpret_cast<uint8_t*>(slots + static_cast<size_t>(nslots) * CT * 64) +
+                   wave * kUnitStageBytes;
+  StreamUnit cur;
+  auto load_unit = [&](int sl) {
+    const int t = min(t0 + sl / U, ntiles - 1), g0 = (sl % U) * kUnit;
+    if constexpr (COAL)
+      stream_load_coal_t<SVEC>(cur, P, K, G, t, g0, lane);
+    else
+      stream_load_t<PACKED, SVEC>(cur, P, K, G, t, g0, lane);
+  };
 
   // x's first batch, then this wave's first slot loads, fly together
   StageBatch sb0;
   stage_load(sb0, X, K, 0, M, 0, K, 0);
-  StreamUnit cur;
-  {
-    const int sl = min(wave, nslots - 1);
-    stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t0 + sl / U, ntiles - 1), (sl % U) * kUnit, lane);
-  }
+  load_unit(min(wave, nslots - 1));
   const u32x4_t* xrow[CT];
   const float* corr = stream_prologue<CT, Act, true>(xs, xrow, X, K, M, wave, i, a, sb0);
 
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int sl = wave; sl < nslots; sl += kStreamWaves) {
-    if (sl != wave)
-      stream_load_t<PACKED, SVEC>(cur, P, K, G, min(t0 + sl / U, ntiles - 1), (sl % U) * kUnit,
-                                  lane);
+    if (sl != wave) load_unit(sl);
     f32x4_t part[CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) part[ct] = zero;
     const int g0 = (sl % U) * kUnit;
-    stream_unit<NR, CT, Layout<Act, PACKED>, true>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
+    if constexpr (COAL) {
+      StreamUnit lay;
+      unit_relayout(lay, cur, stage, lane);
+      stream_unit<NR, CT, Layout<Act, PACKED>, true>(part, lay, xrow, corr, g0, min(kUnit, G - g0), a);
+    } else {
+      stream_unit<NR, CT, Layout<Act, PACKED>, true>(part, cur, xrow, corr, g0, min(kUnit, G - g0), a);
+    }
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) slots[(sl * CT + ct) * 64 + lane] = part[ct];
   }
@@ -1748,7 +1806,16 @@ size_t split_lds_bytes(int K, int M) {
          static_cast<size_t>(split_tiles_per_round(K)) * U * CT * 64 * 16;
 }
 
-bool split_fits(int K, int M) { return M <= 32 && split_lds_bytes(K, M) <= kLdsMax; }
+// LDS of the split kernel: split_lds_bytes plus the file-layout staging
+// rows at one column tile.
+size_t split_kernel_lds(int K, int M, bool packed) {
+  return split_lds_bytes(K, M) +
+         (!packed && M <= 16 ? static_cast<size_t>(kStreamWaves) * kUnitStageBytes : 0);
+}
+
+bool split_fits(int K, int M, bool packed) {
+  return M <= 32 && split_kernel_lds(K, M, packed) <= kLdsMax;
+}
 
 // Resident workgroups per CU of the persistent stream kernels: 3 of the
 // 4-wave one-column-tile kernel, 2 of the 8-wave two-column-tile kernel
@@ -1908,7 +1975,7 @@ int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStrea
     }
     return launch_split_piece<PACKED, NR, SVEC, CT, Act>(P, X, K, M, plan, stream);
   }
-  const size_t lds = split_lds_bytes(K, M);
+  const size_t lds = split_kernel_lds(K, M, PACKED);
   const int ntiles = P.ntiles;
   const int tpr = split_tiles_per_round(K);
   const int grid = (ntiles + tpr - 1) / tpr;
@@ -2028,10 +2095,10 @@ int launch_swiglu(const ProjTable& P, const uint16_t* X, int K, int M, hipStream
 
 // Unit-parallel (split) when the tiles alone leave most of the machine
 // idle and each tile has several units; otherwise tile-serial streaming.
-bool prefer_split(const ProjTable& P, int K, int M) {
+bool prefer_split(const ProjTable& P, int K, int M, bool packed) {
   const int U = (K / kGroup + kUnit - 1) / kUnit;
   return split_piece_plan(P.ntiles, K, M).hg != 0 ||
-         (U >= 2 && split_fits(K, M) && P.ntiles < 2 * cu_count());
+         (U >= 2 && split_fits(K, M, packed) && P.ntiles < 2 * cu_count());
 }
 
 template <bool PACKED, bool SPLIT, class Act = ActBf16>
@@ -2053,7 +2120,7 @@ int launch_stream_any(const ProjTable& P, const uint16_t* X, int K, int M, hipSt
 
 template <bool PACKED, class Act = ActBf16>
 int launch_stream(const ProjTable& P, const uint16_t* X, int K, int M, hipStream_t stream) {
-  return prefer_split(P, K, M) ? launch_stream_any<PACKED, true, Act>(P, X, K, M, stream)
+  return prefer_split(P, K, M, PACKED) ? launch_stream_any<PACKED, true, Act>(P, X, K, M, stream)
                                : launch_stream_any<PACKED, false, Act>(P, X, K, M, stream);
 }
 
@@ -2190,7 +2257,7 @@ int dispatch(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y
       if (!stream_fits(K, M, PACKED)) return CUDALM_W4A16_EVARIANT;
       return launch_stream_any<PACKED, false>(single_table(W, S, Y, N), X, K, M, stream);
     case CUDALM_W4A16_VARIANT_SPLIT:
-      if (!split_fits(K, M) && split_piece_plan((N + kTileRows - 1) / kTileRows, K, M).hg == 0)
+      if (!split_fits(K, M, PACKED) && split_piece_plan((N + kTileRows - 1) / kTileRows, K, M).hg == 0)
         return CUDALM_W4A16_EVARIANT;
       return launch_stream_any<PACKED, true>(single_table(W, S, Y, N), X, K, M, stream);
     case CUDALM_W4A16_VARIANT_TILE16:
