@@ -704,65 +704,76 @@ __device__ __forceinline__ void stream_load_piece(StreamPiece<HG>& h, TileAddr a
   stream_load_scales<HG, PACKED, SVEC>(h, ad, G, g0);
 }
 
-// File-layout pieces of 4 groups in whole lines. In the lane layout the
-// MFMA operand needs (row 16 rt + i, 16 bytes at 64 g + 16 a), every wave
-// load reads 64 B from each of 16 rows; here load q reads rows
-// 16 rt + 4 q .. +3, 256 contiguous bytes each (the piece's 4 groups; lane
-// l: row 4 q + l / 16, byte 16 (l % 16) of the piece), and the step re-lays
-// the piece out through the wave's LDS staging rows (coal_relayout). Rows
-// past the matrix are clamped to its last row, as in tile_addr.
+// File-layout pieces in whole lines. In the lane layout the MFMA operand
+// needs (row 16 rt + i, 16 bytes at 64 g + 16 a), every wave load reads 64 B
+// from each of 16 rows. Here a piece of HG groups (2 or 4) is loaded as
+// HG * 64 contiguous bytes per row: load q reads rows R q .. R q + R - 1 of
+// the tile (R = 16 / HG; lane l: row R q + l / (4 HG), byte 16 (l % 4 HG) of
+// the piece), and coal_relayout moves the piece into the lane layout
+// through the wave's LDS staging rows. Rows past the matrix are clamped to
+// its last row, as in tile_addr.
+template <int HG>
 struct CoalAddr {
-  const uint8_t* w;  // row 16 rt + lane / 16 (clamped) at group 0
-  uint32_t d[3];     // bytes from w to rows +4, +8, +12 (clamped)
-  const uint8_t* s;  // this lane's scale row (row 16 rt + lane % 16), as tile_addr
+  const uint8_t* w;    // row 16 rt + lane / (4 HG) (clamped) at group 0
+  uint32_t d[HG - 1];  // bytes from w to the rows of loads 1 .. HG-1 (clamped)
+  const uint8_t* s;    // this lane's scale row (row 16 rt + lane % 16), as tile_addr
 };
 
-constexpr int kCoalPitch = 272;                       // bytes per staged row: 256 + 16
-constexpr int kCoalStageBytes = kTileRows * kCoalPitch;  // per wave
+// bytes per staged row: the piece + 16 (conflict-free writes and reads)
+template <int HG>
+constexpr int coal_pitch() { return HG * 64 + 16; }
+template <int HG>
+constexpr int coal_stage_bytes() { return kTileRows * coal_pitch<HG>(); }  // per wave
 
-template <class PT>
-__device__ __forceinline__ CoalAddr coal_addr(const PT& P, int K, int G, int t, int lane) {
+template <int HG, class PT>
+__device__ __forceinline__ CoalAddr<HG> coal_addr(const PT& P, int K, int G, int t, int lane) {
+  static_assert(HG == 2 || HG == 4, "whole-line pieces of 2 or 4 groups");
+  constexpr int R = kTileRows / HG;
   const ProjView v = proj_view(P, t);
   const int rt = t - v.begin;
-  const int r0 = rt * kTileRows + (lane >> 4);
+  const int r0 = rt * kTileRows + lane / (4 * HG);
   const int rb = min(r0, v.n - 1);
   const uint32_t rowb = static_cast<uint32_t>(K >> 1);
-  CoalAddr c;
+  CoalAddr<HG> c;
   c.w = v.w + static_cast<size_t>(rb) * rowb;
 #pragma unroll
-  for (int q = 1; q < 4; ++q) c.d[q - 1] = static_cast<uint32_t>(min(r0 + 4 * q, v.n - 1) - rb) * rowb;
+  for (int q = 1; q < HG; ++q)
+    c.d[q - 1] = static_cast<uint32_t>(min(r0 + R * q, v.n - 1) - rb) * rowb;
   const int row = min(rt * kTileRows + (lane & 15), v.n - 1);
   c.s = reinterpret_cast<const uint8_t*>(v.s + static_cast<size_t>(row) * G);
   return c;
 }
 
-template <bool SVEC, bool FULL>
-__device__ __forceinline__ void coal_load_piece(StreamPiece<4>& h, const CoalAddr& ad, int G, int g0,
-                                                int lane) {
-  const int c = lane & 15;
+template <int HG, bool SVEC, bool FULL>
+__device__ __forceinline__ void coal_load_piece(StreamPiece<HG>& h, const CoalAddr<HG>& ad, int G,
+                                                int g0, int lane) {
+  const int c = lane % (4 * HG);
   const uint32_t off = FULL ? static_cast<uint32_t>(g0 * 64 + 16 * c)
                             : static_cast<uint32_t>(min(g0 + (c >> 2), G - 1) * 64 + 16 * (c & 3));
   h.w[0] = load_weights(ad.w + off);
 #pragma unroll
-  for (int q = 1; q < 4; ++q) h.w[q] = load_weights(ad.w + ad.d[q - 1] + off);
-  stream_load_scales<4, false, SVEC>(h, TileAddr{ad.w, ad.s}, G, g0);
+  for (int q = 1; q < HG; ++q) h.w[q] = load_weights(ad.w + ad.d[q - 1] + off);
+  stream_load_scales<HG, false, SVEC>(h, TileAddr{ad.w, ad.s}, G, g0);
 }
 
 // The loaded piece (coalesced layout) into the lane layout, through this
 // wave's staging rows.
-__device__ __forceinline__ void coal_relayout(StreamPiece<4>& out, const StreamPiece<4>& in,
+template <int HG>
+__device__ __forceinline__ void coal_relayout(StreamPiece<HG>& out, const StreamPiece<HG>& in,
                                               uint8_t* stage, int lane) {
+  constexpr int R = kTileRows / HG, P = coal_pitch<HG>();
   const int i = lane & 15, a = lane >> 4;
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-    *reinterpret_cast<u32x4_t*>(stage + (4 * q + (lane >> 4)) * kCoalPitch + 16 * (lane & 15)) = in.w[q];
+  for (int q = 0; q < HG; ++q)
+    *reinterpret_cast<u32x4_t*>(stage + (R * q + lane / (4 * HG)) * P + 16 * (lane % (4 * HG))) =
+        in.w[q];
   wave_lds_sync();
 #pragma unroll
-  for (int gg = 0; gg < 4; ++gg)
-    out.w[gg] = *reinterpret_cast<const u32x4_t*>(stage + i * kCoalPitch + 64 * gg + 16 * a);
+  for (int gg = 0; gg < HG; ++gg)
+    out.w[gg] = *reinterpret_cast<const u32x4_t*>(stage + i * P + 64 * gg + 16 * a);
   wave_lds_sync();  // read before the next piece overwrites the rows
 #pragma unroll
-  for (int q = 0; q < 2; ++q) out.s[q] = in.s[q];
+  for (int q = 0; q < (HG + 1) / 2; ++q) out.s[q] = in.s[q];
 }
 
 template <int HG, int NR, int CT, class Act, bool FULL, bool IOFF = false>
@@ -802,21 +813,21 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
   // File-layout weights of one column tile are loaded in whole lines and
   // re-laid out through per-wave LDS staging rows after the offset table.
   constexpr bool COAL = !PACKED && HG == 4 && CT == 1;
-  using Addr = typename std::conditional<COAL, CoalAddr, TileAddr>::type;
+  using Addr = typename std::conditional<COAL, CoalAddr<HG>, TileAddr>::type;
   auto addr_of = [&](int tt) -> Addr {
     if constexpr (COAL)
-      return coal_addr(P, K, G, tt, lane);
+      return coal_addr<HG>(P, K, G, tt, lane);
     else
       return tile_addr<PACKED>(P, K, G, tt, lane);
   };
   auto load_piece = [&](StreamPiece<HG>& b, const Addr& ad, int g0) {
     if constexpr (COAL)
-      coal_load_piece<SVEC, FULL>(b, ad, G, g0, lane);
+      coal_load_piece<HG, SVEC, FULL>(b, ad, G, g0, lane);
     else
       stream_load_piece<HG, PACKED, SVEC, FULL>(b, ad, G, g0);
   };
   uint8_t* stage = reinterpret_cast<uint8_t*>(xs) + static_cast<size_t>(M) * x_pitch(K) * 16 +
-                   static_cast<size_t>(G) * 64 * CT + wave * kCoalStageBytes;
+                   static_cast<size_t>(G) * 64 * CT + wave * coal_stage_bytes<HG>();
 
   // x's first batch, then the first piece's weights, fly together
   StageBatch sb0;
@@ -861,7 +872,9 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
     // the loads (the scales re-read the current tile's, cached)
     if (!has_next) {
       anx.w = g_piece_sink + lane * 16;
-      if constexpr (COAL) anx.d[0] = anx.d[1] = anx.d[2] = 0;
+      if constexpr (COAL)
+#pragma unroll
+        for (int q = 0; q < HG - 1; ++q) anx.d[q] = 0;
     }
     load_piece(nxt, anx, (has_next ? nh : 0) * HG);
     const int g0 = h * HG;
@@ -1127,7 +1140,13 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
 
   StageBatch sb0;
   if constexpr (!DX) stage_load(sb0, Xc, K, 0, mrows, 0, K, 0);
-  StreamPiece<HG> cur;
+  // file-layout pieces of 2 or 4 groups at one column tile: whole-line
+  // loads into raw, re-laid out into cur through per-wave staging rows
+  // after the scales
+  constexpr bool COAL = !PACKED && CT == 1 && (HG == 2 || HG == 4);
+  uint8_t* stage = reinterpret_cast<uint8_t*>(scs + TPR * NP * U * (PPU - 1) * HG * 16) +
+                   wave * coal_stage_bytes<COAL ? HG : 2>();
+  StreamPiece<HG> cur, raw;
   // DX: the piece's activation fragments, loaded by the wave itself
   u32x4_t xg[DX ? HG : 1][CT][4];
   // slot sl -> row tile t0 + sl / ST, projection (sl % ST) / SP, piece sl % SP
@@ -1140,8 +1159,12 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
       for (int gg = 0; gg < HG; ++gg)
         load_group_x_global<CT>(xg[DX ? gg : 0], Xc, K, mrows, min(h * HG + gg, G - 1), i, a);
     }
-    stream_load_piece<HG, PACKED, SVEC, false>(cur, tile_addr<PACKED>(P, K, G, pj * nt + tf, lane),
-                                               G, h * HG);
+    if constexpr (COAL)
+      coal_load_piece<HG, SVEC, false>(raw, coal_addr<HG>(P, K, G, pj * nt + tf, lane), G, h * HG,
+                                       lane);
+    else
+      stream_load_piece<HG, PACKED, SVEC, false>(cur, tile_addr<PACKED>(P, K, G, pj * nt + tf, lane),
+                                                 G, h * HG);
   };
   load_slot(min(wave, nslots - 1));
   const u32x4_t* xrow[CT];
@@ -1151,6 +1174,7 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
   const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int sl = wave; sl < nslots; sl += WV) {
     if (sl != wave) load_slot(sl);
+    if constexpr (COAL) coal_relayout<HG>(cur, raw, stage, lane);
     const int tu = sl / SP;  // (row tile, projection) pair, local
     const int h = sl % SP;
     const int u = h / PPU, pp = h % PPU;
@@ -1787,7 +1811,7 @@ size_t stream_lds_bytes(int K, int M) {
 size_t stream_kernel_lds(int K, int M, bool packed) {
   const int WV = M > 16 ? 8 : kStreamWaves;
   return stream_lds_bytes(K, M) +
-         (!packed && M <= 16 ? static_cast<size_t>(WV) * kCoalStageBytes : 0);
+         (!packed && M <= 16 ? static_cast<size_t>(WV) * coal_stage_bytes<4>() : 0);
 }
 
 bool stream_fits(int K, int M, bool packed) {
@@ -1903,9 +1927,14 @@ size_t split_piece_lds_bytes(int K, int M, SplitPlan p, int NP = 1) {
   const int U = (K / kGroup + kUnit - 1) / kUnit;
   const int ST = NP * U * PPU;
   const int tpr = ST >= p.wv ? 1 : p.wv / ST;
+  // the file-layout staging rows at one column tile are counted for both
+  // layouts (pieces of 2 or 4 groups)
+  const size_t stage = M <= 16 && (p.hg == 2 || p.hg == 4)
+                           ? static_cast<size_t>(p.wv) * kTileRows * (p.hg * 64 + 16)
+                           : 0;
   return (p.dx ? 0 : static_cast<size_t>(M) * x_pitch(K) * 16) +
          static_cast<size_t>(tpr) * NP * U * CT * 64 * 16 * (1 + (PPU - 1) * p.hg) +
-         static_cast<size_t>(tpr) * NP * U * (PPU - 1) * p.hg * 16 * 4;
+         static_cast<size_t>(tpr) * NP * U * (PPU - 1) * p.hg * 16 * 4 + stage;
 }
 
 SplitPlan split_piece_plan(int ntiles, int K, int M) {
