@@ -24,13 +24,19 @@ pytestmark = pytest.mark.gpu
 CENSUS = [(16, 1024), (512, 1024), (1024, 2048), (1024, 3584), (2048, 1024), (3584, 1024),
           (4096, 1024), (6144, 1024)]
 EDGE = [(1, 128), (3, 128), (5, 256), (9, 1024), (15, 1024), (1023, 1024)]
+# LDS staging rows of the file-layout whole-line loads at M <= 16 (four
+# waves of 16 rows: pieces of 4 groups in the stream kernel, units of 8 in
+# the split kernel); these predicates are for file-layout weights
+_STAGE_STREAM = 4 * 16 * (4 * 64 + 16)
+_STAGE_SPLIT = 4 * 16 * (8 * 64 + 16)
 VARIANTS_FOR_M = {
     # variant name -> predicate on (M, K) for applicability
-    "stream": lambda M, K: M <= 32 and (M * (K // 8 + 1) * 16
-                                        + (K // 128) * 64 * (2 if M > 16 else 1)) <= 160 * 1024,
-    "split": lambda M, K: M <= 32 and (M * (K // 8 + 1) * 16 + (K // 128) * 64 * (2 if M > 16 else 1)
+    "stream": lambda M, K: M <= 32 and (M * (K // 8 + 2) * 16
+                                        + (K // 128) * 64 * (2 if M > 16 else 1)
+                                        + (_STAGE_STREAM if M <= 16 else 0)) <= 160 * 1024,
+    "split": lambda M, K: M <= 32 and (M * (K // 8 + 2) * 16 + (K // 128) * 64 * (2 if M > 16 else 1)
                                        + max(1, 4 // -(-K // 1024)) * -(-K // 1024) * (2 if M > 16 else 1)
-                                       * 1024) <= 160 * 1024,
+                                       * 1024 + (_STAGE_SPLIT if M <= 16 else 0)) <= 160 * 1024,
     "tile16": lambda M, K: True,
     "tile32": lambda M, K: True,
     "prefill": lambda M, K: True,
@@ -467,6 +473,26 @@ def test_two_tile_stream_edges(w4, orc, dev, N, bad, M):
         w4.gemv_prepacked(p, x, N, K, M, y=y, variant="stream")
         assert np.array_equal(down(y).reshape(M, N), ref), ("shift", shift)
         assert torch.isnan(buf[shift + M * N]).item(), ("guard", shift)
+
+
+@pytest.mark.parametrize("N,K", [(1000, 640), (77, 3584), (4100, 2176), (33, 1024), (2050, 2048),
+                                 (248, 4096)])
+@pytest.mark.parametrize("M", [1, 5, 16])
+def test_file_layout_whole_line_loads(w4, orc, dev, N, K, M):
+    # file-layout weights at M <= 16 are loaded in whole lines and re-laid
+    # out through LDS (stream: pieces of 4 groups; split: units of 8; piece
+    # split: pieces of 2 or 4): every variant that applies, bit for bit
+    # against the tile kernel, over ragged last tiles (row clamps) and short
+    # last pieces and units (group clamps: K/128 = 5, 17, 28)
+    W, S = orc.synth_w4a16(0xF1E0 + N + K, N, K)
+    X = orc.synth_act(0xF1E1 + M, M, K)
+    w, s, x = up(dev, W, S, X)
+    ref = run(w4, w, s, x, N, K, M, "tile16")
+    assert_tol(orc, ref, W, S, X, N, K, M, "file-layout")
+    for name in ("auto", "stream", "split"):
+        if name != "auto" and not VARIANTS_FOR_M[name](M, K):
+            continue
+        assert np.array_equal(run(w4, w, s, x, N, K, M, name), ref), name
 
 
 @pytest.mark.parametrize("seed", range(6))
