@@ -186,7 +186,7 @@ int cudalm_w4a16_gemv_bf16_chain(const cudalm_w4a16_stage* stages, int n_stages,
  * cannot allocate device memory (code under graph-capture set-up, tight
  * serving loops, harnesses that forbid hipMalloc). No counterpart in the
  * reference. The plan, flags and counters live in a file-scope device array
- * of the library (4,228,096 bytes per GPU, held until the process ends) that
+ * of the library (4,236,288 bytes per GPU, held until the process ends) that
  * holds up to CUDALM_W4A16_NOALLOC_MAX_STAGES stages; more stages return
  * CUDALM_W4A16_ERANGE. The call allocates nothing (no hipMalloc, no device
  * allocation of any library); it plans (copying the plan into that array and
