@@ -58,6 +58,37 @@ def test_shape_preconditions_rejected_before_device(w4):
     assert w4.gemv_ptr(fake + 1, fake, fake, fake, 4, 128, 1, w4.VARIANT_STREAM) == w4.EVARIANT
 
 
+def test_chain_plan_preconditions_rejected_before_device(w4):
+    # the stage checks of cudalm_w4a16_chain_plan return before any HIP
+    # call, SwiGLU stages (stage.act) included
+    import ctypes
+    lib = w4.lib()
+    fake = 0x100000
+    ws_bytes = lib.cudalm_w4a16_chain_workspace_bytes(1)
+    assert ws_bytes > 0 and lib.cudalm_w4a16_chain_workspace_bytes(0) == 0
+    assert lib.cudalm_w4a16_chain_workspace_bytes(w4.MAX_STAGES + 1) == 0
+
+    def plan(items, K, act, M=4, x=fake):
+        arr = w4.proj_array(items)
+        st = (w4.Stage * 1)()
+        st[0].projs, st[0].count, st[0].x, st[0].K, st[0].dep = \
+            ctypes.cast(arr, ctypes.c_void_p), len(items), x, K, -1
+        st[0].act = act
+        h = w4.ChainHandle()
+        return lib.cudalm_w4a16_chain_plan(ctypes.cast(st, ctypes.c_void_p), 1, M, 1, fake, ws_bytes,
+                                           ctypes.byref(h), None)
+
+    gu = [(fake, None, 0, 3584), (fake, None, 0, 3584)]
+    assert plan(gu[:1], 1024, fake) == w4.EINVAL                      # one projection
+    assert plan(gu + [(fake, None, 0, 3584)], 1024, fake) == w4.EINVAL  # three
+    assert plan([gu[0], (fake, None, 0, 3568)], 1024, fake) == w4.EINVAL  # N differs
+    assert plan(gu, 2176, fake) == w4.EINVAL                          # K > 2048
+    assert plan(gu, 1024, fake + 1) == w4.EALIGN                      # act not 2 B aligned
+    assert plan(gu, 1024, fake, x=fake + 8) == w4.EALIGN              # x not 16 B aligned
+    assert plan([(fake, None, 0, 3584)], 1024, None) == w4.ENULL      # no act: y is required
+    assert plan(gu, 1024, fake, M=33) == w4.EINVAL
+
+
 def test_bf16_gemv_preconditions_rejected_before_device(w4):
     # include/cudalm_bf16_gemv.h: N, K, M >= 1; 2-byte aligned bases; a
     # forced stream variant needs K % 8 == 0 and 16 B bases
