@@ -281,6 +281,9 @@ def main():
                     help="headline workload only (for counter collection)")
     ap.add_argument("--bf16-lm-head-only", action="store_true",
                     help="only the tied bf16 LM head lines (for counter collection)")
+    ap.add_argument("--file-lm-head-only", action="store_true",
+                    help="only the W4A16 LM head through the file-layout entry, M = 1 then"
+                         " M = 8 (for counter collection)")
     ap.add_argument("--cfg0-mib", type=int, default=2048,
                     help="MiB of weight copies the configs[0] line rotates over (profiler runs: 320)")
     ap.add_argument("--only", default="", choices=["", "config0", "lm_head_m8", "lm_head_m32"],
@@ -332,6 +335,25 @@ def main():
     if args.bf16_lm_head_only:
         print(json.dumps({"bf16_lm_head": bench_bf16_lm_head(torch, lib, dev, stream, sraw,
                                                              reps=args.steps)}), flush=True)
+        return
+
+    if args.file_lm_head_only:
+        # the drop-in call on the file's row-major weights (no repack), over
+        # the same rotating copies as the headline
+        N, K = LM_HEAD
+        fw = [synth_weights(torch, N, K, 0x11AD + c, dev) for c in range(args.copies)]
+        res = {}
+        for Mf in (1, 8):
+            xf = synth_act(torch, Mf, K, 0x11AE + Mf, dev)
+            yf = torch.empty((Mf, N), dtype=torch.bfloat16, device=dev)
+            lf = [(lambda w=w, s=s, xf=xf, yf=yf, Mf=Mf: lib.cudalm_w4a16_gemv_bf16(
+                w.data_ptr(), s.data_ptr(), xf.data_ptr(), yf.data_ptr(), N, K, Mf, sraw))
+                  for w, s in fw]
+            t = stream_time(torch, lf, args.steps, args.warmup, stream)
+            nb = algo_bytes(N, K, Mf)
+            res[f"M{Mf}"] = {"kernel_us": round(t * 1e6, 2), "GBps": round(nb / t / 1e9, 1),
+                             "frac_hbm_peak": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
+        print(json.dumps({"file_layout_lm_head": res}), flush=True)
         return
 
     # ---------------- headline: LM head, M = 1, prepacked ----------------
