@@ -52,7 +52,8 @@ struct Bf16Unit {
 // MFMA steps) is written to the wave's staging rows and read back in operand
 // layout just before its steps. Rows are kStagePitch bytes apart (128 B of
 // data + 16 B) so the 16 rows' operand reads spread over the LDS banks.
-// Measured on the LM head (N = 248320, K = 1024, M = 1): 88.4 -> 79.2 us.
+// Measured on the LM head (N = 248320, K = 1024, M = 1): 88.4 -> 77.6 us
+// (with the sink below).
 // Read-only target of a wave's last, unused unit load (both layouts):
 // one unit (8 slabs of 1 KB), never written. The loop's loads stay
 // unconditional without re-reading a non-temporally loaded unit from HBM.
@@ -161,7 +162,8 @@ __global__ __launch_bounds__(kWaves * 64) void bf16_gemv_stream_kernel(
   if (t >= ntiles) return;
 
   // this wave's staging rows (row-major weights), after the activations
-  uint8_t* stage = reinterpret_cast<uint8_t*>(xs + static_cast<size_t>(mc) * pitch) + wave * kStageBytes;
+  uint8_t* stage =
+      reinterpret_cast<uint8_t*>(xs + static_cast<size_t>(mc) * pitch) + wave * kStageBytes;
   const u32x4_t* xrow[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) xrow[ct] = xs + min(ct * 16 + i, mrows - 1) * pitch;

@@ -52,8 +52,8 @@
 //     and the stage proceeds, so every wave exits; the host reads the word
 //     with cudalm_w4a16_chain_status.
 // Flags and epochs are written with vector stores, the error word with a
-// vector atomic. The grid is the number of workgroups that are resident at once, so
-// no workgroup waits on one that cannot be scheduled.
+// vector atomic. The grid is the number of workgroups that are resident at
+// once, so no workgroup waits on one that cannot be scheduled.
 //
 // Measured per stage of the M = 1 census chain (s_memrealtime probes, one
 // box): last flag of stage s-1 -> stage s's wait done 1.4 us; x loaded and
