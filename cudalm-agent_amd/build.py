@@ -26,6 +26,8 @@ HIPCC_FLAGS = [
     "-fPIC",
     # packed fp32 VALU ops are kept out of all device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # kernel arguments preloaded into SGPRs at dispatch (first 16 dwords)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     # explicit fp32 operation sequence: no mul+add contraction
     "-ffp-contract=off",
     "-fno-strict-aliasing",
@@ -103,6 +105,8 @@ def build_boundary_check(verbose: bool = False) -> str:
     rpath = "$ORIGIN/" + os.path.relpath(os.path.dirname(LIB), os.path.dirname(CHECK_BIN))
     cmd = [hipcc(), "--offload-arch=gfx950", "-O2", "-std=c++17",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # kernel arguments preloaded into SGPRs at dispatch (first 16 dwords)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
            "-Wno-unused-command-line-argument", "-I", os.path.join(REPO, "include"), CHECK_SRC,
            "-L", os.path.dirname(LIB), "-lcudalm_w4a16", f"-Wl,-rpath,{rpath}", "-o", CHECK_BIN + ".tmp"]
     if verbose:

@@ -267,6 +267,26 @@ using ProjTable = ProjTab<kMaxProj>;
 using ProjOne = ProjTab<1>;
 using ProjFour = ProjTab<4>;
 
+// Single-projection launches pass the projection as scalar kernel
+// arguments. The library is built with -amdgpu-kernarg-preload-count=16,
+// so the first 16 argument dwords arrive preloaded in SGPRs when the
+// dispatcher supports it, and the first weight loads do not wait for a
+// kernel-argument fetch through the cold scalar cache (a by-value struct
+// argument is not preloaded). Census launches: 607 -> 593 us per token
+// unfused at M = 1, 495 -> 478 us fused at M = 8.
+__device__ __forceinline__ ProjOne make_proj_one(const uint8_t* w, const uint16_t* s, uint16_t* y,
+                                                 int n, int ntiles) {
+  ProjOne P;
+  P.w[0] = w;
+  P.s[0] = s;
+  P.y[0] = y;
+  P.n[0] = n;
+  P.tile_end[0] = ntiles;
+  P.count = 1;
+  P.ntiles = ntiles;
+  return P;
+}
+
 // The projection that owns tile t. Every field is read at a constant
 // offset and chosen with scalar selects, so the kernel-argument loads are
 // independent of each other (a data-dependent index would chain three
@@ -788,10 +808,10 @@ __device__ __forceinline__ void stream_piece(f32x4_t (&part)[CT], const StreamPi
   }
 }
 
-template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, int HG = 4, bool FULL = true,
-          int WV = kStreamWaves, bool IOFF = false, class PT = ProjTable>
-__global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
-    const PT P, const uint16_t* __restrict__ X, int K, int M, int pwg, int t_static) {
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, bool FULL, int WV, bool IOFF,
+          class PT>
+__device__ __forceinline__ void stream_piece_body(
+    const PT& P, const uint16_t* __restrict__ X, int K, int M, int pwg, int t_static) {
   extern __shared__ u32x4_t xs[];
   constexpr int PPU = kUnit / HG;  // pieces per 8-group unit
   const int G = K >> 7;
@@ -920,14 +940,29 @@ __global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
   }
 }
 
+template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, int HG = 4, bool FULL = true,
+          int WV = kStreamWaves, bool IOFF = false, class PT = ProjTable>
+__global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_kernel(
+    const PT P, const uint16_t* __restrict__ X, int K, int M, int pwg, int t_static) {
+  stream_piece_body<PACKED, NR, SVEC, CT, Act, HG, FULL, WV, IOFF, PT>(P, X, K, M, pwg, t_static);
+}
+
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, bool FULL, int WV, bool IOFF>
+__global__ __launch_bounds__(WV * 64) void w4a16_stream_piece_one_kernel(
+    const uint8_t* w, const uint16_t* s, uint16_t* y, int n, int ntiles,
+    const uint16_t* __restrict__ X, int K, int M, int pwg, int t_static) {
+  stream_piece_body<PACKED, NR, SVEC, CT, Act, HG, FULL, WV, IOFF, ProjOne>(
+      make_proj_one(w, s, y, n, ntiles), X, K, M, pwg, t_static);
+}
+
 // Split kernel: few weight tiles, several units per tile (K >= 2048). A
 // workgroup takes TPR = max(1, 4/U) tiles; its waves compute the unit
 // partials of those tiles side by side, park them in LDS, and the unit
 // partials of each tile are summed in unit order. Same bits as the stream
 // kernel; shorter latency when tiles alone cannot fill the machine.
-template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, class PT = ProjTable>
-__global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
-    const PT P, const uint16_t* __restrict__ X, int K, int M) {
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, class PT>
+__device__ __forceinline__ void split_body(const PT& P, const uint16_t* __restrict__ X, int K,
+                                           int M) {
   extern __shared__ u32x4_t xs[];
   const int G = K >> 7;
   const int pitch = x_pitch(K);
@@ -990,6 +1025,19 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
     }
     store_tile<NR, CT, Act, PT, PACKED>(P, t0 + wave, total, M, i, a, X, K);
   }
+}
+
+template <bool PACKED, int NR, bool SVEC, int CT, class Act = ActBf16, class PT = ProjTable>
+__global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_kernel(
+    const PT P, const uint16_t* __restrict__ X, int K, int M) {
+  split_body<PACKED, NR, SVEC, CT, Act, PT>(P, X, K, M);
+}
+
+template <bool PACKED, int NR, bool SVEC, int CT, class Act>
+__global__ __launch_bounds__(kStreamWaves * 64) void w4a16_split_one_kernel(
+    const uint8_t* w, const uint16_t* s, uint16_t* y, int n, int ntiles,
+    const uint16_t* __restrict__ X, int K, int M) {
+  split_body<PACKED, NR, SVEC, CT, Act, ProjOne>(make_proj_one(w, s, y, n, ntiles), X, K, M);
 }
 
 // ---------------------------------------------------------------------------
@@ -1109,10 +1157,10 @@ __global__ __launch_bounds__(kStreamWaves * 64) void w4a16_swiglu_kernel(
 // up tile nt + t, and the output is silu(gate) * up on the bf16-rounded
 // projections (blockIdx.y walks chunks of mc activation rows).
 
-template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, int NP = 1,
-          bool DX = false, class PT = ProjTable>
-__global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
-    const PT P, const uint16_t* __restrict__ X, int K, int M, int mc) {
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, int NP, bool DX,
+          class PT>
+__device__ __forceinline__ void split_piece_body(
+    const PT& P, const uint16_t* __restrict__ X, int K, int M, int mc) {
   extern __shared__ u32x4_t xs[];
   constexpr int PPU = kUnit / HG;
   const int G = K >> 7;
@@ -1281,6 +1329,21 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
         }
     }
   }
+}
+
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, int NP = 1,
+          bool DX = false, class PT = ProjTable>
+__global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
+    const PT P, const uint16_t* __restrict__ X, int K, int M, int mc) {
+  split_piece_body<PACKED, NR, SVEC, CT, Act, HG, WV, NP, DX, PT>(P, X, K, M, mc);
+}
+
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, bool DX>
+__global__ __launch_bounds__(WV * 64) void w4a16_split_piece_one_kernel(
+    const uint8_t* w, const uint16_t* s, uint16_t* y, int n, int ntiles,
+    const uint16_t* __restrict__ X, int K, int M) {
+  split_piece_body<PACKED, NR, SVEC, CT, Act, HG, WV, 1, DX, ProjOne>(
+      make_proj_one(w, s, y, n, ntiles), X, K, M, M);
 }
 
 // ---------------------------------------------------------------------------
@@ -1875,22 +1938,25 @@ int launch_stream_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStre
   // 4.30 -> 4.10 us); waves that stream many tiles share the table (inline
   // chains cost the LM head 0.9 us at M = 1 and 3.6 us at M = 8).
   const bool ioff = ntiles <= grid * WV;
-  auto go = [&](const auto& T) {
-    using PT = std::decay_t<decltype(T)>;
-    auto kern =
-        ioff ? (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, true, PT>
-                           : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, true, PT>)
-             : (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, false, PT>
-                           : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, false, PT>);
-    if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, T, X, K, M, grid, ntiles);
-    return launch_status();
-  };
   if (P.count == 1) {
-    const ProjOne one = shrink_table<1>(P);
-    return go(one);
+    auto kern =
+        ioff ? (G % 4 == 0 ? w4a16_stream_piece_one_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, true>
+                           : w4a16_stream_piece_one_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, true>)
+             : (G % 4 == 0 ? w4a16_stream_piece_one_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, false>
+                           : w4a16_stream_piece_one_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, false>);
+    if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P.w[0], P.s[0], P.y[0], P.n[0],
+                       ntiles, X, K, M, grid, ntiles);
+    return launch_status();
   }
-  return go(P);
+  auto kern =
+      ioff ? (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, true>
+                         : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, true>)
+           : (G % 4 == 0 ? w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, true, WV, false>
+                         : w4a16_stream_piece_kernel<PACKED, NR, SVEC, CT, Act, 4, false, WV, false>);
+  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M, grid, ntiles);
+  return launch_status();
 }
 
 // Piece split plan: HG groups per piece, WV waves per workgroup; hg = 0
@@ -1958,6 +2024,13 @@ int launch_split_piece_t(const PT& P, const uint16_t* X, int K, int M, hipStream
   const int tpr = SP >= WV ? 1 : WV / SP;
   const size_t lds = split_piece_lds_bytes(K, M, SplitPlan{HG, WV, DX});
   const int grid = (P.ntiles + tpr - 1) / tpr;
+  if constexpr (std::is_same<PT, ProjOne>::value) {
+    auto kern = w4a16_split_piece_one_kernel<PACKED, NR, SVEC, CT, Act, HG, WV, DX>;
+    if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P.w[0], P.s[0], P.y[0],
+                       P.n[0], P.ntiles, X, K, M);
+    return launch_status();
+  }
   auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, Act, HG, WV, 1, DX, PT>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P, X, K, M, M);
@@ -2009,10 +2082,10 @@ int launch_split_t(const ProjTable& P, const uint16_t* X, int K, int M, hipStrea
   const int tpr = split_tiles_per_round(K);
   const int grid = (ntiles + tpr - 1) / tpr;
   if (P.count == 1) {
-    const ProjOne one = shrink_table<1>(P);
-    auto kern = w4a16_split_kernel<PACKED, NR, SVEC, CT, Act, ProjOne>;
+    auto kern = w4a16_split_one_kernel<PACKED, NR, SVEC, CT, Act>;
     if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(kStreamWaves * 64), lds, stream, one, X, K, M);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kStreamWaves * 64), lds, stream, P.w[0], P.s[0],
+                       P.y[0], P.n[0], P.ntiles, X, K, M);
     return launch_status();
   }
   auto kern = w4a16_split_kernel<PACKED, NR, SVEC, CT, Act>;
