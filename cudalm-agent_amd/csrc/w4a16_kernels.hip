@@ -1338,6 +1338,41 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_kernel(
   split_piece_body<PACKED, NR, SVEC, CT, Act, HG, WV, NP, DX, PT>(P, X, K, M, mc);
 }
 
+// Up to four projections sharing x, as scalar arguments: the first 16
+// dwords (weights, tile ends, count, x, K, M) are what the first loads of a
+// prepacked launch need; scales, outputs and row counts follow.
+template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, bool DX>
+__global__ __launch_bounds__(WV * 64) void w4a16_split_piece_four_kernel(
+    const uint8_t* w0, const uint8_t* w1, const uint8_t* w2, const uint8_t* w3, int te0, int te1,
+    int te2, int count, const uint16_t* __restrict__ X, int K, int M, const uint16_t* s0,
+    const uint16_t* s1, const uint16_t* s2, const uint16_t* s3, uint16_t* y0, uint16_t* y1,
+    uint16_t* y2, uint16_t* y3, int n0, int n1, int n2, int n3, int ntiles) {
+  ProjFour P;
+  P.w[0] = w0;
+  P.w[1] = w1;
+  P.w[2] = w2;
+  P.w[3] = w3;
+  P.s[0] = s0;
+  P.s[1] = s1;
+  P.s[2] = s2;
+  P.s[3] = s3;
+  P.y[0] = y0;
+  P.y[1] = y1;
+  P.y[2] = y2;
+  P.y[3] = y3;
+  P.n[0] = n0;
+  P.n[1] = n1;
+  P.n[2] = n2;
+  P.n[3] = n3;
+  P.tile_end[0] = te0;
+  P.tile_end[1] = te1;
+  P.tile_end[2] = te2;
+  P.tile_end[3] = ntiles;
+  P.count = count;
+  P.ntiles = ntiles;
+  split_piece_body<PACKED, NR, SVEC, CT, Act, HG, WV, 1, DX, ProjFour>(P, X, K, M, M);
+}
+
 template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, bool DX>
 __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_one_kernel(
     const uint8_t* w, const uint16_t* s, uint16_t* y, int n, int ntiles,
@@ -2029,6 +2064,15 @@ int launch_split_piece_t(const PT& P, const uint16_t* X, int K, int M, hipStream
     if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P.w[0], P.s[0], P.y[0],
                        P.n[0], P.ntiles, X, K, M);
+    return launch_status();
+  }
+  if constexpr (std::is_same<PT, ProjFour>::value) {
+    auto kern = w4a16_split_piece_four_kernel<PACKED, NR, SVEC, CT, Act, HG, WV, DX>;
+    if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(WV * 64), lds, stream, P.w[0], P.w[1], P.w[2],
+                       P.w[3], P.tile_end[0], P.tile_end[1], P.tile_end[2], P.count, X, K, M,
+                       P.s[0], P.s[1], P.s[2], P.s[3], P.y[0], P.y[1], P.y[2], P.y[3], P.n[0],
+                       P.n[1], P.n[2], P.n[3], P.ntiles);
     return launch_status();
   }
   auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, Act, HG, WV, 1, DX, PT>;
