@@ -1373,6 +1373,29 @@ __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_four_kernel(
   split_piece_body<PACKED, NR, SVEC, CT, Act, HG, WV, 1, DX, ProjFour>(P, X, K, M, M);
 }
 
+// The SwiGLU pair (NP = 2: gate, then up, sharing x; act into y0), as
+// scalar arguments, the first 16 dwords being what the first loads need.
+template <bool PACKED, int NR, bool SVEC, int CT, int HG, int WV, bool DX>
+__global__ __launch_bounds__(WV * 64) void w4a16_split_piece_pair_kernel(
+    const uint8_t* w0, const uint8_t* w1, int nt, int count, const uint16_t* __restrict__ X, int K,
+    int M, int mc, const uint16_t* s0, const uint16_t* s1, uint16_t* y0, uint16_t* y1, int n0,
+    int n1, int ntiles) {
+  ProjTab<2> P;
+  P.w[0] = w0;
+  P.w[1] = w1;
+  P.s[0] = s0;
+  P.s[1] = s1;
+  P.y[0] = y0;
+  P.y[1] = y1;
+  P.n[0] = n0;
+  P.n[1] = n1;
+  P.tile_end[0] = nt;
+  P.tile_end[1] = ntiles;
+  P.count = count;
+  P.ntiles = ntiles;
+  split_piece_body<PACKED, NR, SVEC, CT, ActBf16, HG, WV, 2, DX, ProjTab<2>>(P, X, K, M, mc);
+}
+
 template <bool PACKED, int NR, bool SVEC, int CT, class Act, int HG, int WV, bool DX>
 __global__ __launch_bounds__(WV * 64) void w4a16_split_piece_one_kernel(
     const uint8_t* w, const uint16_t* s, uint16_t* y, int n, int ntiles,
@@ -2202,9 +2225,11 @@ int launch_swiglu_piece_t(const ProjTable& P, const uint16_t* X, int K, int M, i
   const int gx = (P.tile_end[0] + tpr - 1) / tpr;
   const int gy = (M + mc - 1) / mc;
   if (gy > 65535) return CUDALM_W4A16_ERANGE;
-  auto kern = w4a16_split_piece_kernel<PACKED, NR, SVEC, CT, ActBf16, HG, WV, 2, DX>;
+  auto kern = w4a16_split_piece_pair_kernel<PACKED, NR, SVEC, CT, HG, WV, DX>;
   if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
-  hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(WV * 64), lds, stream, P, X, K, M, mc);
+  hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(WV * 64), lds, stream, P.w[0], P.w[1], P.tile_end[0],
+                     P.count, X, K, M, mc, P.s[0], P.s[1], P.y[0], P.y[1], P.n[0], P.n[1],
+                     P.ntiles);
   return launch_status();
 }
 
