@@ -709,7 +709,7 @@ def main():
                      "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
                      "traffic_source": "profiles/w4a16_stream_lm_head_M1.md (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0, copy-calibrated)",
-                     "kernel": "w4a16_stream_piece_kernel<true, 1, false, 1, ActBf16, 4, true, 4, false, ProjTab<1> >",
+                     "kernel": "w4a16_stream_piece_one_kernel<true, 1, false, 1, ActBf16, 4, true, 4, false>",
                      "kernel_us": round(kern_s * 1e6, 3),
                      "kernel_us_source": "HIP events around the timed K launches / K",
                      "kernel_us_event_pairs": round(per_launch * 1e6, 3),
