@@ -148,7 +148,7 @@ template <bool PACKED>
 int launch_prefill32(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                      int K, int M, hipStream_t stream);
 
-// Registers per lane of that kernel (prepacked instance).
+// Registers per lane of that kernel at K = 1024 (prepacked instance).
 int prefill32_regs();
 
 }  // namespace cudalm_hip

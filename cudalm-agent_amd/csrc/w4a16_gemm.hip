@@ -33,6 +33,9 @@
 // of the unit's (group, 16-row) pairs into an LDS table, and each wave
 // decodes its 32 rows' weights once per k-block and runs MT chains per
 // group. Weights of the unit are loaded before the x staging completes.
+// At K = 1024 (one unit) w4a16_gemm32_split_kernel runs instead: the
+// unit's groups are split over two wave sets, which hand the canonical fma
+// chain from one to the other through LDS.
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -279,6 +282,215 @@ __global__ __launch_bounds__(WVN * 64) void w4a16_gemm32_kernel(
   }
 }
 
+// K = 1024 (one 8-group unit): the unit's groups split over two wave sets.
+// A workgroup of 2 x WVN waves owns 32 WVN weight rows and 32 activation
+// rows; wave (ks, wn) loads and decodes the weights of groups 4 ks .. 4 ks + 3
+// of rows 32 wn .. 32 wn + 31 and runs their offset-seeded chains. Set 0
+// folds its four chain results into part = fma(s, tmp, part) in group order
+// and hands part to set 1 through LDS; set 1 holds its four results in
+// registers and continues the same fma chain with groups 4..7, then stores.
+// The arithmetic is that of w4a16_gemm32_kernel, step for step; each wave
+// has half the weight loads and half the chains on its critical path.
+constexpr int kSplitHalf = kUnit / 2;  // groups per wave set
+
+template <int WVN>
+constexpr size_t gemm32_split_lds_bytes() {
+  return gemm32_lds_bytes<WVN, 1>() + static_cast<size_t>(WVN) * 64 * 16 * 4;
+}
+
+template <int WVN, bool PACKED, bool SVEC>
+__global__ __launch_bounds__(WVN * 2 * 64) void w4a16_gemm32_split_kernel(
+    const uint8_t* __restrict__ W, const uint16_t* __restrict__ S,
+    const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, int N, int M) {
+  constexpr int K = kUnit * kGroup;
+  constexpr int G = kUnit;
+  constexpr int NW = 2 * WVN;  // waves per workgroup
+  constexpr int NT = NW * 64;
+  constexpr int TM = 32;
+  extern __shared__ u32x4_t lds[];  // x [TM][kPB], offset table [8][TM] f32, part exchange
+  u32x4_t* xs = lds;
+  float* corr = reinterpret_cast<float*>(lds + TM * kPB);
+  f32x4_t* xchg = reinterpret_cast<f32x4_t*>(corr + kUnit * TM);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int ks = wave / WVN, wn = wave - ks * WVN;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int j = lane & 31, h = lane >> 5;
+  const int i16 = lane & 15, a16 = lane >> 4;
+  const int m0 = blockIdx.y * TM;
+  const int mrows = min(TM, M - m0);
+  const int n = (blockIdx.x * WVN + wn) * 32 + j;
+  const bool wave_ok = (blockIdx.x * WVN + wn) * 32 < N;
+  const int gb = ks * kSplitHalf;  // this wave set's first group
+
+  // activations first (loads return in issue order), then the weights and
+  // scales of this wave set's groups
+  constexpr int NBLK = TM * kUnit * 16;
+  static_assert(NBLK % NT == 0 && NT % (kUnit * 16) == 0, "staging covers the tile exactly");
+  constexpr int BPT = NBLK / NT;
+  constexpr int RS = NT / (kUnit * 16);
+  const int b = tid & (kUnit * 16 - 1);
+  const int r0 = tid / (kUnit * 16);
+  u32x4_t v[BPT];
+  {
+    const uint16_t* xcol = X + static_cast<size_t>(m0) * K + 8 * b;
+#pragma unroll
+    for (int q = 0; q < BPT; ++q)
+      v[q] = *reinterpret_cast<const u32x4_t*>(xcol +
+                                               static_cast<size_t>(min(r0 + q * RS, mrows - 1)) * K);
+  }
+  u32x4_t wl[kSplitHalf], wh[kSplitHalf];
+  uint32_t sc[kSplitHalf / 2];
+  {
+    const int row = min(n, N - 1);
+    const uint8_t* w_lo;
+    const uint8_t* s_row;
+    int step;
+    if constexpr (PACKED) {
+      const uint8_t* tile = W + static_cast<size_t>(row >> 4) * packed_tile_bytes(G);
+      w_lo = tile + 16 * (16 * h + (row & 15));
+      s_row = tile + static_cast<size_t>(G) * 1024 + (row & 15) * packed_scale_pitch(G);
+      step = 1024;
+    } else {
+      w_lo = W + static_cast<size_t>(row) * (K >> 1) + 16 * h;
+      s_row = reinterpret_cast<const uint8_t*>(S + static_cast<size_t>(row) * G);
+      step = 64;
+    }
+    const uint8_t* w_hi = w_lo + (PACKED ? 16 * 32 : 32);
+#pragma unroll
+    for (int gg = 0; gg < kSplitHalf; ++gg) {
+      wl[gg] = *reinterpret_cast<const u32x4_t*>(w_lo + (gb + gg) * step);
+      wh[gg] = *reinterpret_cast<const u32x4_t*>(w_hi + (gb + gg) * step);
+    }
+    if constexpr (PACKED || SVEC) {
+      const uint2 sv = *reinterpret_cast<const uint2*>(s_row + 2 * gb);
+      sc[0] = sv.x;
+      sc[1] = sv.y;
+    } else {
+      const uint16_t* srow = reinterpret_cast<const uint16_t*>(s_row);
+#pragma unroll
+      for (int q = 0; q < kSplitHalf / 2; ++q)
+        sc[q] = static_cast<uint32_t>(srow[gb + 2 * q]) |
+                (static_cast<uint32_t>(srow[gb + 2 * q + 1]) << 16);
+    }
+  }
+  {
+    u32x4_t* xdst = xs + r0 * kPB + b;
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) xdst[q * RS * kPB] = pair_order(v[q]);
+  }
+  __syncthreads();
+  // offset table: 16 chains (group, 16-row tile) split over the waves
+  {
+    constexpr int NCH = kUnit * 2;
+    constexpr int CPW = (NCH + NW - 1) / NW;
+    u32x4_t xo[CPW][4];
+#pragma unroll
+    for (int q = 0; q < CPW; ++q) {
+      const int c = min(wave + q * NW, NCH - 1);
+      const u32x4_t* xg = xs + ((c & 1) * 16 + i16) * kPB + (c >> 1) * 16 + 4 * a16;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) xo[q][d] = xg[d];
+    }
+#pragma unroll
+    for (int q = 0; q < CPW; ++q) {
+      const int c = wave + q * NW;
+      const f32x4_t o = group_offset(xo[q]);
+      if (c < NCH && i16 == 0)
+        *reinterpret_cast<f32x4_t*>(corr + (c >> 1) * TM + (c & 1) * 16 + 4 * a16) = o;
+    }
+  }
+  __syncthreads();
+
+  // chain results of this wave set's groups
+  f32x16_t t[kSplitHalf];
+  if (wave_ok) {
+#pragma unroll
+    for (int gq = 0; gq < kSplitHalf; ++gq) {
+      const int gg = gb + gq;
+      u32x4_t xa[4][2];
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) xa[d][e] = xs[j * kPB + gg * 16 + 4 * (2 * e + h) + d];
+      const float* cr = corr + gg * TM + 4 * h;
+      f32x16_t acc;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4_t o4 = *reinterpret_cast<const f32x4_t*>(cr + 8 * q);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[4 * q + r] = o4[r];
+      }
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          acc = mfma32(xa[d][e], decode_nibbles<PACKED>(e == 0 ? wl[gq][d] : wh[gq][d]), acc);
+      t[gq] = acc;
+    }
+  }
+  const auto scale = [&](int gq) {
+    return half_bits_to_f32((sc[gq >> 1] >> (16 * (gq & 1))) & 0xFFFFu);
+  };
+  f32x4_t* slot = xchg + wn * 4 * 64 + lane;
+  if (ks == 0 && wave_ok) {
+    f32x16_t part = {};
+#pragma unroll
+    for (int gq = 0; gq < kSplitHalf; ++gq) {
+      const float s = scale(gq);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) part[r] = __builtin_fmaf(s, t[gq][r], part[r]);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      slot[q * 64] = f32x4_t{part[4 * q], part[4 * q + 1], part[4 * q + 2], part[4 * q + 3]};
+  }
+  __syncthreads();
+  if (ks == 0 || !wave_ok || n >= N) return;
+  f32x16_t part;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const f32x4_t p4 = slot[q * 64];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part[4 * q + r] = p4[r];
+  }
+#pragma unroll
+  for (int gq = 0; gq < kSplitHalf; ++gq) {
+    const float s = scale(gq);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[r] = __builtin_fmaf(s, t[gq][r], part[r]);
+  }
+  // one unit: total = 0 + part
+  const f32x16_t zero16 = {};
+  const f32x16_t total = zero16 + part;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+    if (m < mrows) {
+      float val = 16.0f * total[r];
+      if (__builtin_expect(val != val, 0))
+        val = w4a16_ref_dot<PACKED>(W, S, K, n, X + static_cast<size_t>(m0 + m) * K);
+      Y[static_cast<size_t>(m0 + m) * N + n] = static_cast<uint16_t>(f32_to_bf16_rne(val));
+    }
+  }
+}
+
+template <int WVN, bool PACKED>
+int launch_gemm32_split(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
+                        int M, hipStream_t stream) {
+  const size_t lds = gemm32_split_lds_bytes<WVN>();
+  const int gx = (N + 32 * WVN - 1) / (32 * WVN);
+  const int gy = (M + 31) / 32;
+  if (gy > 65535) return CUDALM_W4A16_ERANGE;
+  const bool svec = !PACKED && aligned(S, 8);
+  auto kern = svec ? w4a16_gemm32_split_kernel<WVN, PACKED, true>
+                   : w4a16_gemm32_split_kernel<WVN, PACKED, false>;
+  if (!allow_lds(kern, lds)) return CUDALM_W4A16_ELAUNCH;
+  hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(WVN * 2 * 64), lds, stream, W, S, X, Y, N, M);
+  return launch_status();
+}
+
 template <int WVN, int MT, int NB, bool PACKED>
 int launch_gemm32(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                   int K, int M, hipStream_t stream) {
@@ -299,10 +511,11 @@ int launch_gemm32(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16
 template <bool PACKED>
 int launch_prefill32(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                      int K, int M, hipStream_t stream) {
+  if (K == kUnit * kGroup) return launch_gemm32_split<8, PACKED>(W, S, X, Y, N, M, stream);
   return launch_gemm32<8, 1, 1, PACKED>(W, S, X, Y, N, K, M, stream);
 }
 
-int prefill32_regs() { return regs_of(w4a16_gemm32_kernel<8, 1, 1, true, false>); }
+int prefill32_regs() { return regs_of(w4a16_gemm32_split_kernel<8, true, false>); }
 
 template int launch_prefill32<true>(const uint8_t*, const uint16_t*, const uint16_t*, uint16_t*,
                                     int, int, int, hipStream_t);

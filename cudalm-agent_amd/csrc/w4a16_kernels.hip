@@ -2671,7 +2671,7 @@ int cudalm_w4a16_kernel_regs(int variant) {
   switch (variant) {
     case CUDALM_W4A16_VARIANT_AUTO:
     case CUDALM_W4A16_VARIANT_STREAM:
-      return regs_of(w4a16_stream_piece_kernel<true, 1, false, 1, ActBf16, 4, true>);
+      return regs_of(w4a16_stream_piece_one_kernel<true, 1, false, 1, ActBf16, 4, true, 4, false>);
     case CUDALM_W4A16_VARIANT_TILE16: return regs_of(w4a16_tile_kernel<1, 1, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_TILE32: return regs_of(w4a16_tile_kernel<1, 2, 4, 1, 8, true>);
     case CUDALM_W4A16_VARIANT_PREFILL: return regs_of(w4a16_gemm_unit_kernel<1, 2, 8, true, false>);

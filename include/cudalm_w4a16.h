@@ -269,7 +269,8 @@ int cudalm_w4a16_gemv_bf16_prepacked_variant(const void* packed,
 
 /* VGPR + AGPR count of a variant's kernel, -1 if unavailable (AUTO and
  * STREAM: the M = 1 stream kernel; PREFILL: the 16x16 unit GEMM of 128 x 32
- * tiles; PREFILL32: the 32x32 GEMM). Replaces
+ * tiles; PREFILL32: the 32x32 GEMM at K = 1024, whose groups are split over
+ * two wave sets). Replaces
  * int4_gemv_bf16_rowtile4_regs (int4_gemv_bf16.h:52) and
  * batch_int4_gemv_bf16_rowtile4_regs (batch_decode.h:67). */
 int cudalm_w4a16_kernel_regs(int variant);
