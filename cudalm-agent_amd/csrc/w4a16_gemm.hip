@@ -511,8 +511,30 @@ int launch_gemm32(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16
 template <bool PACKED>
 int launch_prefill32(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                      int K, int M, hipStream_t stream) {
-  if (K == kUnit * kGroup) return launch_gemm32_split<8, PACKED>(W, S, X, Y, N, M, stream);
+  if (K == kUnit * kGroup) {
+    switch (prefill_split_waves(N, M, cu_count())) {
+      case 2: return launch_gemm32_split<2, PACKED>(W, S, X, Y, N, M, stream);
+      case 4: return launch_gemm32_split<4, PACKED>(W, S, X, Y, N, M, stream);
+      default: return launch_gemm32_split<8, PACKED>(W, S, X, Y, N, M, stream);
+    }
+  }
   return launch_gemm32<8, 1, 1, PACKED>(W, S, X, Y, N, K, M, stream);
+}
+
+// Waves per wave set of the K = 1024 split kernel: the narrowest of 2, 4
+// and 8 (64, 128 or 256 weight rows per workgroup) whose workgroups fill
+// between half and one round of the CUs; 0 when none does. M = 512: 512 x
+// 1024 takes 2 (5.20-5.25 against 5.51-5.56 us for the 64 x 32 unit GEMM),
+// 2048 x 1024 takes 4 (6.57 against 6.68-6.75 us for the 128 x 32 one),
+// 3584 and 4096 x 1024 take 8; 6144 x 1024 fits no round and keeps the unit
+// GEMM (13.8-14.1 against 15.9-16.4 us).
+int prefill_split_waves(int N, int M, int cus) {
+  const long long gy = (M + 31) / 32;
+  for (int wv = 2; wv <= 8; wv *= 2) {
+    const long long wgs = gy * ((N + 32 * wv - 1) / (32 * wv));
+    if (2 * wgs >= cus && wgs <= cus) return wv;
+  }
+  return 0;
 }
 
 int prefill32_regs() { return regs_of(w4a16_gemm32_split_kernel<8, true, false>); }

@@ -6,7 +6,9 @@ both weight layouts. Outputs must equal the tile kernel's bit for bit (the
 per-output operation sequence every kernel shares: each 16 x 16 x 32 MFMA
 step equals two 32 x 32 x 16 steps over its k-block halves) and be within
 the oracle's bound (the restatement of tests/cuda/test_int4_gemv_bf16.cpp:
-54-69). Every row equals the single-row call on it."""
+54-69). Every row equals the single-row call on it. At K = 1024 the
+split kernel runs with wave sets of 8 (3584 x 512, 1000 x 70), 2
+(2048 x 129) and 4 (2000 x 500) waves on a 256-CU part."""
 import numpy as np
 import pytest
 import torch
@@ -22,7 +24,7 @@ def _bits(t):
 @pytest.mark.parametrize("N,K,M", [(3584, 1024, 512), (4096, 1024, 512), (1000, 1024, 70),
                                    (16, 1024, 33), (2048, 1024, 129), (1024, 3584, 100),
                                    (1024, 2048, 64), (37, 384, 40), (300, 2176, 97),
-                                   (1, 128, 33), (257, 1024, 1)])
+                                   (1, 128, 33), (257, 1024, 1), (2000, 1024, 500)])
 def test_prefill32_bit_identity(w4, orc, dev, N, K, M):
     W, S = orc.synth_w4a16(0x919E + N + M + K, N, K)
     X = orc.synth_act(0x919F + M, M, K)
