@@ -293,9 +293,25 @@ __global__ __launch_bounds__(WVN * 64) void w4a16_gemm32_kernel(
 // has half the weight loads and half the chains on its critical path.
 constexpr int kSplitHalf = kUnit / 2;  // groups per wave set
 
-template <int WVN>
+// File layout: each wave loads its rows' 256-byte run of the set's four
+// groups in whole lines (load q: rows 4q .. 4q + 3, lane l: bytes 16 (l % 16)
+// of row 4q + l / 16) and re-lays them out for the MFMA lanes through a
+// per-wave LDS staging area, half the run at a time (rows of 144 bytes).
+// With 2-wave sets the staging would leave room for one workgroup per CU
+// instead of two, so those keep 32-byte loads straight into the lanes.
+constexpr int kSplitStagePitch = 144;
+
+template <int WVN, bool PACKED>
+constexpr bool split_staged() {
+  return !PACKED && WVN >= 4;
+}
+
+template <int WVN, bool PACKED>
 constexpr size_t gemm32_split_lds_bytes() {
-  return gemm32_lds_bytes<WVN, 1>() + static_cast<size_t>(WVN) * 64 * 16 * 4;
+  // the part hand-over (WVN x 4 KB) reuses the file layout's staging area
+  return gemm32_lds_bytes<WVN, 1>() +
+         (split_staged<WVN, PACKED>() ? static_cast<size_t>(2 * WVN) * 32 * kSplitStagePitch
+                                      : static_cast<size_t>(WVN) * 64 * 16 * 4);
 }
 
 template <int WVN, bool PACKED, bool SVEC>
@@ -307,10 +323,12 @@ __global__ __launch_bounds__(WVN * 2 * 64) void w4a16_gemm32_split_kernel(
   constexpr int NW = 2 * WVN;  // waves per workgroup
   constexpr int NT = NW * 64;
   constexpr int TM = 32;
+  constexpr bool STAGED = split_staged<WVN, PACKED>();
   extern __shared__ u32x4_t lds[];  // x [TM][kPB], offset table [8][TM] f32, part exchange
   u32x4_t* xs = lds;
   float* corr = reinterpret_cast<float*>(lds + TM * kPB);
-  f32x4_t* xchg = reinterpret_cast<f32x4_t*>(corr + kUnit * TM);
+  uint8_t* stage = reinterpret_cast<uint8_t*>(corr + kUnit * TM);
+  f32x4_t* xchg = reinterpret_cast<f32x4_t*>(stage);
 
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
@@ -341,27 +359,36 @@ __global__ __launch_bounds__(WVN * 2 * 64) void w4a16_gemm32_split_kernel(
                                                static_cast<size_t>(min(r0 + q * RS, mrows - 1)) * K);
   }
   u32x4_t wl[kSplitHalf], wh[kSplitHalf];
+  u32x4_t raw[8];  // file layout: the whole-line loads, before the re-layout
   uint32_t sc[kSplitHalf / 2];
   {
     const int row = min(n, N - 1);
-    const uint8_t* w_lo;
     const uint8_t* s_row;
-    int step;
     if constexpr (PACKED) {
       const uint8_t* tile = W + static_cast<size_t>(row >> 4) * packed_tile_bytes(G);
-      w_lo = tile + 16 * (16 * h + (row & 15));
+      const uint8_t* w_lo = tile + 16 * (16 * h + (row & 15));
       s_row = tile + static_cast<size_t>(G) * 1024 + (row & 15) * packed_scale_pitch(G);
-      step = 1024;
-    } else {
-      w_lo = W + static_cast<size_t>(row) * (K >> 1) + 16 * h;
-      s_row = reinterpret_cast<const uint8_t*>(S + static_cast<size_t>(row) * G);
-      step = 64;
-    }
-    const uint8_t* w_hi = w_lo + (PACKED ? 16 * 32 : 32);
 #pragma unroll
-    for (int gg = 0; gg < kSplitHalf; ++gg) {
-      wl[gg] = *reinterpret_cast<const u32x4_t*>(w_lo + (gb + gg) * step);
-      wh[gg] = *reinterpret_cast<const u32x4_t*>(w_hi + (gb + gg) * step);
+      for (int gg = 0; gg < kSplitHalf; ++gg) {
+        wl[gg] = *reinterpret_cast<const u32x4_t*>(w_lo + (gb + gg) * 1024);
+        wh[gg] = *reinterpret_cast<const u32x4_t*>(w_lo + 16 * 32 + (gb + gg) * 1024);
+      }
+    } else if constexpr (!STAGED) {
+      const uint8_t* w_lo = W + static_cast<size_t>(row) * (K >> 1) + 16 * h;
+      s_row = reinterpret_cast<const uint8_t*>(S + static_cast<size_t>(row) * G);
+#pragma unroll
+      for (int gg = 0; gg < kSplitHalf; ++gg) {
+        wl[gg] = *reinterpret_cast<const u32x4_t*>(w_lo + (gb + gg) * 64);
+        wh[gg] = *reinterpret_cast<const u32x4_t*>(w_lo + 32 + (gb + gg) * 64);
+      }
+    } else {
+      s_row = reinterpret_cast<const uint8_t*>(S + static_cast<size_t>(row) * G);
+      const int rbase = (blockIdx.x * WVN + wn) * 32 + (lane >> 4);
+      const uint8_t* wcol = W + gb * 64 + 16 * (lane & 15);
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        raw[q] = *reinterpret_cast<const u32x4_t*>(
+            wcol + static_cast<size_t>(min(rbase + 4 * q, N - 1)) * (K >> 1));
     }
     if constexpr (PACKED || SVEC) {
       const uint2 sv = *reinterpret_cast<const uint2*>(s_row + 2 * gb);
@@ -403,6 +430,31 @@ __global__ __launch_bounds__(WVN * 2 * 64) void w4a16_gemm32_split_kernel(
   }
   __syncthreads();
 
+  if constexpr (STAGED) {
+    // re-lay the wave's rows out for the MFMA lanes: lane (j, h) takes
+    // 16-byte chunks 4 gq + h (groups' k 32h .. 32h + 31) and 4 gq + 2 + h
+    // of row j
+    uint8_t* st = stage + wave * 32 * kSplitStagePitch;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      if (((lane >> 3) & 1) == hh) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          *reinterpret_cast<u32x4_t*>(st + (4 * q + (lane >> 4)) * kSplitStagePitch +
+                                      (lane & 7) * 16) = raw[q];
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int g2 = 0; g2 < 2; ++g2) {
+        wl[2 * hh + g2] =
+            *reinterpret_cast<const u32x4_t*>(st + j * kSplitStagePitch + (4 * g2 + h) * 16);
+        wh[2 * hh + g2] =
+            *reinterpret_cast<const u32x4_t*>(st + j * kSplitStagePitch + (4 * g2 + 2 + h) * 16);
+      }
+      wave_lds_sync();
+    }
+  }
+
   // chain results of this wave set's groups
   f32x16_t t[kSplitHalf];
   if (wave_ok) {
@@ -434,21 +486,23 @@ __global__ __launch_bounds__(WVN * 2 * 64) void w4a16_gemm32_split_kernel(
     return half_bits_to_f32((sc[gq >> 1] >> (16 * (gq & 1))) & 0xFFFFu);
   };
   f32x4_t* slot = xchg + wn * 4 * 64 + lane;
+  f32x16_t part = {};
   if (ks == 0 && wave_ok) {
-    f32x16_t part = {};
 #pragma unroll
     for (int gq = 0; gq < kSplitHalf; ++gq) {
       const float s = scale(gq);
 #pragma unroll
       for (int r = 0; r < 16; ++r) part[r] = __builtin_fmaf(s, t[gq][r], part[r]);
     }
+  }
+  if constexpr (STAGED) __syncthreads();  // every wave is done with its staging rows
+  if (ks == 0 && wave_ok) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       slot[q * 64] = f32x4_t{part[4 * q], part[4 * q + 1], part[4 * q + 2], part[4 * q + 3]};
   }
   __syncthreads();
   if (ks == 0 || !wave_ok || n >= N) return;
-  f32x16_t part;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const f32x4_t p4 = slot[q * 64];
@@ -479,7 +533,7 @@ __global__ __launch_bounds__(WVN * 2 * 64) void w4a16_gemm32_split_kernel(
 template <int WVN, bool PACKED>
 int launch_gemm32_split(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                         int M, hipStream_t stream) {
-  const size_t lds = gemm32_split_lds_bytes<WVN>();
+  const size_t lds = gemm32_split_lds_bytes<WVN, PACKED>();
   const int gx = (N + 32 * WVN - 1) / (32 * WVN);
   const int gy = (M + 31) / 32;
   if (gy > 65535) return CUDALM_W4A16_ERANGE;
