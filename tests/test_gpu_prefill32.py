@@ -48,3 +48,31 @@ def test_prefill32_bit_identity(w4, orc, dev, N, K, M):
         y1 = torch.empty((1, N), dtype=torch.bfloat16, device=dev)
         w4.gemv(w, s, x[b:b + 1], N, K, 1, y=y1)
         assert np.array_equal(Y[b], _bits(y1).reshape(N)), b
+
+
+@pytest.mark.parametrize("N,M", [(3584, 512), (2000, 500), (2048, 129), (1000, 40)])
+def test_prefill_scale_base_not_8_aligned(w4, orc, dev, N, M):
+    # file-layout scales whose base is 2 bytes past an 8-byte boundary: the
+    # K = 1024 split kernel (wave sets of 8, 4 and 2 waves; the last shape
+    # takes the unit GEMM) reads them one at a time instead of 8 bytes per
+    # row. Same bits as with aligned scales, for the shape's dispatch and the
+    # forced 32x32 variant.
+    K = 1024
+    W, S = orc.synth_w4a16(0x5CA1 + N + M, N, K)
+    X = orc.synth_act(0x5CA2 + M, M, K)
+    w = torch.from_numpy(W).to(dev)
+    s = torch.from_numpy(S.view(np.int16)).to(dev).view(torch.float16)
+    x = torch.from_numpy(X.view(np.int16)).to(dev).view(torch.bfloat16)
+    buf = torch.empty(N * (K // 128) + 4, dtype=torch.float16, device=dev)
+    s_mis = buf[1:1 + N * (K // 128)].view(N, K // 128)
+    s_mis.copy_(s)
+    assert s_mis.data_ptr() % 8 != 0
+    for variant in ("auto", "prefill32"):
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        w4.gemv(w, s, x, N, K, M, y=y, variant=variant)
+        ym = torch.empty_like(y)
+        w4.gemv(w, s_mis, x, N, K, M, y=ym, variant=variant)
+        assert np.array_equal(_bits(y), _bits(ym)), (variant, N, M)
+    yt = torch.empty_like(y)
+    w4.gemv(w, s, x, N, K, M, y=yt, variant="tile32")
+    assert np.array_equal(_bits(ym), _bits(yt)), ("tile32", N, M)
