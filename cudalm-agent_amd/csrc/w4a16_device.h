@@ -149,8 +149,8 @@ int launch_prefill32(const uint8_t* W, const uint16_t* S, const uint16_t* X, uin
                      int K, int M, hipStream_t stream);
 
 // Waves per wave set of the K = 1024 split 32x32 kernel for an N x 1024 x M
-// GEMM on `cus` CUs, 0 when its workgroups would not fill half to one round.
-int prefill_split_waves(int N, int M, int cus);
+// GEMM on `cus` CUs, 0 when the unit GEMM serves the shape better.
+int prefill_split_waves(int N, int M, int cus, bool packed);
 
 // Registers per lane of that kernel at K = 1024 (prepacked instance).
 int prefill32_regs();

@@ -306,12 +306,21 @@ constexpr bool split_staged() {
   return !PACKED && WVN >= 4;
 }
 
+// 4-wave sets without staging hand part over through the activation buffer
+// (after a barrier every reader of it has passed): 67 KB of LDS, two
+// workgroups per CU.
+template <int WVN, bool PACKED>
+constexpr bool split_alias() {
+  return WVN == 4 && !split_staged<WVN, PACKED>();
+}
+
 template <int WVN, bool PACKED>
 constexpr size_t gemm32_split_lds_bytes() {
   // the part hand-over (WVN x 4 KB) reuses the file layout's staging area
   return gemm32_lds_bytes<WVN, 1>() +
          (split_staged<WVN, PACKED>() ? static_cast<size_t>(2 * WVN) * 32 * kSplitStagePitch
-                                      : static_cast<size_t>(WVN) * 64 * 16 * 4);
+          : split_alias<WVN, PACKED>() ? static_cast<size_t>(0)
+                                       : static_cast<size_t>(WVN) * 64 * 16 * 4);
 }
 
 template <int WVN, bool PACKED, bool SVEC>
@@ -328,7 +337,8 @@ __global__ __launch_bounds__(WVN * 2 * 64) void w4a16_gemm32_split_kernel(
   u32x4_t* xs = lds;
   float* corr = reinterpret_cast<float*>(lds + TM * kPB);
   uint8_t* stage = reinterpret_cast<uint8_t*>(corr + kUnit * TM);
-  f32x4_t* xchg = reinterpret_cast<f32x4_t*>(stage);
+  constexpr bool ALIAS = split_alias<WVN, PACKED>();
+  f32x4_t* xchg = reinterpret_cast<f32x4_t*>(ALIAS ? reinterpret_cast<uint8_t*>(lds) : stage);
 
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
@@ -495,7 +505,8 @@ __global__ __launch_bounds__(WVN * 2 * 64) void w4a16_gemm32_split_kernel(
       for (int r = 0; r < 16; ++r) part[r] = __builtin_fmaf(s, t[gq][r], part[r]);
     }
   }
-  if constexpr (STAGED) __syncthreads();  // every wave is done with its staging rows
+  // every wave is done with its staging rows / the activations
+  if constexpr (STAGED || ALIAS) __syncthreads();
   if (ks == 0 && wave_ok) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
@@ -566,7 +577,7 @@ template <bool PACKED>
 int launch_prefill32(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N,
                      int K, int M, hipStream_t stream) {
   if (K == kUnit * kGroup) {
-    switch (prefill_split_waves(N, M, cu_count())) {
+    switch (prefill_split_waves(N, M, cu_count(), PACKED)) {
       case 2: return launch_gemm32_split<2, PACKED>(W, S, X, Y, N, M, stream);
       case 4: return launch_gemm32_split<4, PACKED>(W, S, X, Y, N, M, stream);
       default: return launch_gemm32_split<8, PACKED>(W, S, X, Y, N, M, stream);
@@ -577,17 +588,22 @@ int launch_prefill32(const uint8_t* W, const uint16_t* S, const uint16_t* X, uin
 
 // Waves per wave set of the K = 1024 split kernel: the narrowest of 2, 4
 // and 8 (64, 128 or 256 weight rows per workgroup) whose workgroups fill
-// between half and one round of the CUs; 0 when none does. M = 512: 512 x
-// 1024 takes 2 (5.20-5.25 against 5.51-5.56 us for the 64 x 32 unit GEMM),
-// 2048 x 1024 takes 4 (6.57 against 6.68-6.75 us for the 128 x 32 one),
-// 3584 and 4096 x 1024 take 8; 6144 x 1024 fits no round and keeps the unit
-// GEMM (13.8-14.1 against 15.9-16.4 us).
-int prefill_split_waves(int N, int M, int cus) {
+// between half and one round of the CUs. M = 512: 512 x 1024 takes 2
+// (5.20-5.25 against 5.51-5.56 us for the 64 x 32 unit GEMM), 2048 x 1024
+// takes 4 (6.57 against 6.68-6.75 us for the 128 x 32 one), 3584 and 4096
+// x 1024 take 8. When none fits, prepacked weights take 4-wave sets (two
+// workgroups per CU) from one to 1.5 rounds of those: 6144 x 1024 13.48-13.61
+// against 14.37-14.63 us for the unit GEMM; the file layout, whose 4-wave
+// sets stage their loads and run one workgroup per CU, keeps the unit GEMM
+// (15.9-16.0 against 19.1-19.3 us). 0: the unit GEMM.
+int prefill_split_waves(int N, int M, int cus, bool packed) {
   const long long gy = (M + 31) / 32;
   for (int wv = 2; wv <= 8; wv *= 2) {
     const long long wgs = gy * ((N + 32 * wv - 1) / (32 * wv));
     if (2 * wgs >= cus && wgs <= cus) return wv;
   }
+  const long long wgs4 = gy * ((N + 127) / 128);
+  if (packed && wgs4 >= cus && wgs4 <= 3LL * cus) return 4;
   return 0;
 }
 

@@ -2367,7 +2367,7 @@ template <bool PACKED>
 int launch_prefill(const uint8_t* W, const uint16_t* S, const uint16_t* X, uint16_t* Y, int N, int K,
                    int M, hipStream_t stream) {
   const int cus = cu_count();
-  if (K == kUnit * kGroup && prefill_split_waves(N, M, cus) != 0)
+  if (K == kUnit * kGroup && prefill_split_waves(N, M, cus, PACKED) != 0)
     return launch_prefill32<PACKED>(W, S, X, Y, N, K, M, stream);
   if (K < kUnit * kGroup) {
     const long long wgs32 = static_cast<long long>((N + 255) / 256) * ((M + 31) / 32);
